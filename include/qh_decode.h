@@ -1,0 +1,219 @@
+/*
+ * qh_decode.h -- C ABI of the MI355X (gfx950) batch-1 decode datapath for the
+ * Qwen3.5-0.8B-shaped hybrid model (24 layers = [Gated DeltaNet x3, gated GQA
+ * attention x1] x6, hidden 1024, tied 248320x1024 int8 head).
+ *
+ * Every entry point is extern "C", takes plain pointers and sizes, and returns
+ * an int status: 0 on success, a negative QH_E* code for an argument / format
+ * error detected on the host, or a positive hipError_t value for a HIP runtime
+ * failure.  Op-level functions keep the names and argument order of the
+ * reference's HLS kernels (namespace qwen in the hls/src headers) with a qh_ prefix;
+ * fixed-size arrays become flat row-major device pointers and every function
+ * takes a trailing stream (a hipStream_t, or NULL for the null stream).  Op
+ * pointers are DEVICE pointers owned by the caller.  The ops keep no static
+ * state and are reentrant; calls on one stream run in order.
+ *
+ * Layouts (all row-major, fp32 unless noted):
+ *   int8 GEMV weight   w[out][in] int8, per-output-row scale[out]
+ *   DeltaNet state     S[16][128][128]   (k-major: S[h][k][v])
+ *   conv history       state[6144][4]    (column 0 kept, unused, as in the reference)
+ *   KV cache           kcache/vcache [T_max][2][256] (token-major, kv head, dim)
+ *
+ * The engine keeps the packed int8 blob written by scripts/pack_weights.py
+ * (tensors in kernel read order, 4 KiB aligned, int8 [out,in] followed by fp32
+ * [out] scales) resident in HBM, owns all decode state, and replays one decode
+ * step as a hipGraph.
+ */
+#ifndef QH_DECODE_H
+#define QH_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------- */
+#define QH_OK 0
+#define QH_EINVAL (-1)   /* bad argument (null pointer, bad size)          */
+#define QH_ERANGE (-2)   /* token id / position / context out of range      */
+#define QH_EIO (-3)      /* file open / read / mmap failure                 */
+#define QH_EFORMAT (-4)  /* weight index or blob does not match the layout  */
+#define QH_ENOMEM (-5)   /* host or device allocation failed                */
+#define QH_ESTATE (-6)   /* engine not in a state that allows the call      */
+
+/* ---- model dimensions (hls/src/types.hpp:20-44) ----------------------- */
+#define QH_HIDDEN 1024
+#define QH_N_LAYERS 24
+#define QH_INTER 3584
+#define QH_VOCAB 248320
+#define QH_LH 16         /* DeltaNet heads            */
+#define QH_LK 128        /* DeltaNet key head dim     */
+#define QH_LV 128        /* DeltaNet value head dim   */
+#define QH_CONV_DIM 6144
+#define QH_CONV_K 4
+#define QH_Z_DIM 2048
+#define QH_NH 8          /* attention query heads     */
+#define QH_NKV 2         /* attention kv heads        */
+#define QH_HD 256        /* attention head dim        */
+#define QH_Q_PROJ 4096   /* query + output gate, interleaved per head */
+#define QH_KV_PROJ 512
+#define QH_ROPE_DIM 64
+#define QH_N_TENSORS 320 /* entries in weights.idx    */
+
+/* activation precision of the engine's / layer ops' projections */
+#define QH_MODE_W8A16 0  /* int8 weights x fp32 activations (hls/src csim semantics) */
+#define QH_MODE_W8A8 1   /* int8 weights x per-vector int8 activations, int32 accumulate
+                            (golden/model.py with ACT_INT8 = True) */
+
+/* Tensor view into a weight blob (hls/src/types.hpp:51-56 Tensor).  int8
+ * tensors set w_i8 + scale, fp32 tensors set w_f32.  Device pointers. */
+typedef struct qh_tensor {
+  const int8_t* w_i8;
+  const float* scale;
+  const float* w_f32;
+  int out;
+  int in;
+} qh_tensor;
+
+const char* qh_strerror(int status);
+
+/* ======================================================================
+ * Op level.  Each replaces the HLS C++ function cited beside it.
+ * ==================================================================== */
+
+/* y[o] = (sum_i float(w[o,i]) * x[i]) * scale[o]            gemv.hpp:28-42 gemv_i8 */
+int qh_gemv_i8(float* y, const int8_t* w, const float* scale, const float* x, int out, int in,
+               void* stream);
+/* y = W x with fp32 W                                       gemv.hpp:46-59 gemv_f32 */
+int qh_gemv_f32(float* y, const float* w, const float* x, int out, int in, void* stream);
+/* *result = (sum_i float(w[row,i]) * h[i]) * scale[row]     gemv.hpp:63-73 row_dot_i8
+ * (the reference returns the float; here it is written to a device scalar) */
+int qh_row_dot_i8(float* result, const int8_t* w, const float* scale, const float* h, int row,
+                  int in, void* stream);
+/* h[i] = float(w[tok,i]) * scale[tok]                        gemv.hpp:76-84 embed_row
+ * (tok < 0 -> QH_ERANGE; like the reference, the upper bound is the caller's) */
+int qh_embed_row(float* h, const int8_t* w, const float* scale, int tok, int in, void* stream);
+/* y = x * (1/sqrt(mean(x^2) + eps)) * (1 + w)                norm.hpp:13-20 rmsnorm */
+int qh_rmsnorm(float* y, const float* x, const float* w, int n, float eps, void* stream);
+/* y = x * (1/sqrt(mean(x^2) + eps)) * w * silu(z)           norm.hpp:25-33 rmsnorm_gated */
+int qh_rmsnorm_gated(float* y, const float* x, const float* w, const float* z, int n, float eps,
+                     void* stream);
+/* depthwise causal conv, width 4, then SiLU; state[6144][4]  conv1d.hpp:17-38 conv1d_step */
+int qh_conv1d_step(float* out, const float* in_ch, float* state, const float* weight, void* stream);
+/* cos/sin[64] for a position (theta 1e7, halves mirrored)    rope.hpp:17-27 rope_cos_sin */
+int qh_rope_cos_sin(int pos, float* cos_o, float* sin_o, void* stream);
+/* rotate dims 0..63 of one 256-dim head in place             rope.hpp:30-41 apply_rope */
+int qh_apply_rope(float* x, const float* cos_, const float* sin_, void* stream);
+/* v *= 1/sqrt(sum(v^2) + 1e-6)                               deltanet.hpp:131-136 l2norm */
+int qh_l2norm(float* v, int n, void* stream);
+/* one head of the gated delta rule; S[128][128] updated      deltanet.hpp:58-115 delta_rule_head */
+int qh_delta_rule_head(const float* q, const float* k, const float* v, float g, float beta, float* S,
+                       float* out, void* stream);
+/* all 16 heads; q,k,v,out [16][128]; g,beta [16]; S[16][128][128]
+ *                                                            deltanet.hpp:118-127 delta_rule_layer */
+int qh_delta_rule_layer(const float* q, const float* k, const float* v, const float* g,
+                        const float* beta, float* S, float* out, void* stream);
+/* full Gated DeltaNet decode step, x already input-normed    deltanet.hpp:141-182 deltanet_layer
+ * rec[16][128][128] and conv_state[6144][4] are updated in place. */
+int qh_deltanet_layer(float* out, const float* x, const qh_tensor* qkv_w, const qh_tensor* z_w,
+                      const qh_tensor* b_w, const qh_tensor* a_w, const float* conv_w,
+                      const float* A_log, const float* dt_bias, const float* gate_norm_w,
+                      const qh_tensor* out_w, float* rec, float* conv_state, void* stream);
+/* gated GQA attention decode step                            attention.hpp:25-95 attention_layer
+ * kcache/vcache hold T past tokens as [T][512]; slot T is written; attends over T+1.
+ * Unlike the reference (sc[8192]) any T up to the caller's buffer is accepted. */
+int qh_attention_layer(float* out, const float* x, const qh_tensor* q_w, const qh_tensor* k_w,
+                       const qh_tensor* v_w, const qh_tensor* o_w, const float* q_norm,
+                       const float* k_norm, int pos, float* kcache, float* vcache, int T,
+                       void* stream);
+/* SwiGLU MLP: down(silu(gate x) * up x)                      mlp.hpp:11-19 mlp_layer */
+int qh_mlp_layer(float* out, const float* x, const qh_tensor* gate_w, const qh_tensor* up_w,
+                 const qh_tensor* down_w, void* stream);
+
+/* ---- W8A8 (int8 activation) entry points; no C++ counterpart in hls/src ----
+ * per-vector symmetric int8: s = amax/127 (1 if amax == 0), q = rint(x/s) clipped to +-127.
+ *                          golden/model.py:37-45 _qa; scripts/export_gemv_tv.py:25-30 q_i8_vec */
+int qh_quant_act(int8_t* xq, float* sx, const float* x, int n, void* stream);
+/* acc[o] = sum_i w[o,i]*xq[i] in int32; y[o] = float(acc[o]) * sx * scale[o]
+ * (acc may be NULL)              rtl/gemv_i8.sv:52-72; scripts/export_gemv_tv.py:49-50 */
+int qh_gemv_i8_w8a8(float* y, int32_t* acc, const int8_t* w, const float* scale, const int8_t* xq,
+                    const float* sx, int out, int in, void* stream);
+/* The three layer ops with the projections' inputs quantized where golden/model.py
+ * applies _qa (model.py:143,191 / 200,230 / 234,237). Same arguments as above. */
+int qh_deltanet_layer_w8a8(float* out, const float* x, const qh_tensor* qkv_w, const qh_tensor* z_w,
+                           const qh_tensor* b_w, const qh_tensor* a_w, const float* conv_w,
+                           const float* A_log, const float* dt_bias, const float* gate_norm_w,
+                           const qh_tensor* out_w, float* rec, float* conv_state, void* stream);
+int qh_attention_layer_w8a8(float* out, const float* x, const qh_tensor* q_w, const qh_tensor* k_w,
+                            const qh_tensor* v_w, const qh_tensor* o_w, const float* q_norm,
+                            const float* k_norm, int pos, float* kcache, float* vcache, int T,
+                            void* stream);
+int qh_mlp_layer_w8a8(float* out, const float* x, const qh_tensor* gate_w, const qh_tensor* up_w,
+                      const qh_tensor* down_w, void* stream);
+
+/* ======================================================================
+ * Weight blob layout (scripts/pack_weights.py:25-101, emit_weight_index.py:13-22)
+ * ==================================================================== */
+
+/* Total bytes of the packed blob (758,618,112 for the 0.8B shape). */
+size_t qh_blob_size(void);
+/* Writes the weights.idx text of the canonical layout ("name off nbytes dtype
+ * scale_off scale_nbytes out in" per line).  Returns the number of bytes needed
+ * (excluding the NUL); writes at most cap bytes when buf is not NULL. */
+size_t qh_layout_idx_text(char* buf, size_t cap);
+/* Fills a host buffer of qh_blob_size() bytes with seeded synthetic weights in
+ * the packed layout (int8 U{-127..127}, scales U[1e-3,1e-2], fp32 tensors per
+ * tensor role).  Deterministic in (seed); padding bytes are zero. */
+int qh_synth_blob(void* blob, size_t len, uint64_t seed);
+/* Seeded fills used by benchmarks and tests (SplitMix64 stream `key`). */
+int qh_synth_fill_i8(int8_t* dst, size_t n, uint64_t key);                   /* U{-127..127} */
+int qh_synth_fill_uniform(float* dst, size_t n, uint64_t key, float lo, float hi);
+int qh_synth_fill_normal(float* dst, size_t n, uint64_t key, float mean, float stddev);
+
+/* ======================================================================
+ * Engine: the decode top (hls/src/qwen_synth.hpp:39-92 qwen_top,
+ * hls/src/decoder.hpp:62-120 decode_token) with device-resident state.
+ * ==================================================================== */
+typedef struct qh_engine qh_engine;
+
+/* mmap `blob_path` (run_hls.cpp:27-35) and upload it; `idx_path` (may be NULL)
+ * is a weights.idx whose every line must equal the canonical layout
+ * (tb_decode.cpp:47-65).  max_ctx bounds the KV cache (tokens, >= 1). */
+int qh_engine_create(const char* blob_path, const char* idx_path, int max_ctx, qh_engine** out);
+/* Same from a host buffer (copied to the device; the caller may free it). */
+int qh_engine_create_from_memory(const void* blob, size_t blob_len, const char* idx_text,
+                                 int max_ctx, qh_engine** out);
+int qh_engine_destroy(qh_engine* e);
+/* QH_MODE_W8A16 (default) or QH_MODE_W8A8. */
+int qh_engine_set_mode(qh_engine* e, int mode);
+/* Zero recurrent/conv state, empty KV cache, pos = 0 (state.hpp:24-34). */
+int qh_engine_reset(qh_engine* e);
+/* Decode one token (qwen_top): returns the argmax (ties -> lowest id) in
+ * *argmax_out and, if logits is not NULL, all QH_VOCAB logits into the HOST
+ * buffer `logits`.  Advances pos by one. */
+int qh_decode_token(qh_engine* e, int tok, float* logits, int* argmax_out);
+/* The run_hls loop (run_hls.cpp:56-66) on the device: feed n_prompt ids, then
+ * greedily generate up to n_new ids, stopping before emitting `eos` (eos < 0:
+ * never).  out_ids receives the generated ids, *n_out their count.  The token
+ * feedback stays on the device; the host only launches step graphs. */
+int qh_generate(qh_engine* e, const int* prompt, int n_prompt, int n_new, int eos, int* out_ids,
+                int* n_out);
+/* Tokens processed so far (DecodeState::pos). */
+int qh_engine_pos(const qh_engine* e);
+/* Argmax of the most recent completed step (the next greedy token). */
+int qh_engine_last_argmax(const qh_engine* e);
+/* Run layers [l0, l1) of one decode step on a device hidden vector h (in place,
+ * [1024]) without embed / final norm / head; state and pos advance as in a
+ * full step.  Used for the 4-layer block configuration. */
+int qh_engine_forward_layers(qh_engine* e, int l0, int l1, float* h);
+/* Device pointers of engine-owned buffers (for parity checks):
+ * which = 0 blob, 1 rec state [18][16][128][128], 2 conv state [18][6144][4],
+ * 3 K cache [6][max_ctx][512], 4 V cache [6][max_ctx][512], 5 hidden h [1024]. */
+void* qh_engine_device_ptr(qh_engine* e, int which);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QH_DECODE_H */

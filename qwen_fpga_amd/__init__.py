@@ -1,0 +1,386 @@
+"""Host-side mirror of the reference decode datapath's operator interface.
+
+The reference (allthingssecurity/qwen_fpga) exposes its decode datapath as HLS
+C++ functions in ``namespace qwen`` (hls/src/*.hpp) plus the ``qwen_top`` decode
+top and the ``run_hls`` CLI.  This module binds the MI355X C ABI
+(``include/qh_decode.h``, implemented in ``libqh.so``) with ctypes and keeps the
+same operator names and argument order:
+
+    gemv_i8(y, w, scale, x, out, in)            hls/src/gemv.hpp:28
+    rmsnorm(y, x, w, n, eps)                    hls/src/norm.hpp:13
+    deltanet_layer(out, x, qkv_w, ...)          hls/src/deltanet.hpp:141
+    Engine.decode_token(tok, want_logits)       hls/src/qwen_synth.hpp:39 qwen_top
+    ...
+
+Array arguments are torch tensors already on the GPU (``device="cuda"``); only
+their data pointers cross the boundary.  ``Tensor`` mirrors the reference's
+``qwen::Tensor`` view (types.hpp:51-56).  A non-zero status from the library is
+raised as ``QHError``.  There is no CPU fallback: importing the ops without the
+built library raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libqh.so")
+HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "qh_decode.h")
+
+HIDDEN, N_LAYERS, INTER, VOCAB = 1024, 24, 3584, 248320
+LH, LK, LV, CONV_DIM, CONV_K, Z_DIM = 16, 128, 128, 6144, 4, 2048
+NH, NKV, HD, Q_PROJ, KV_PROJ, ROPE_DIM = 8, 2, 256, 4096, 512, 64
+EPS = 1e-6
+MODE_W8A16, MODE_W8A8 = 0, 1
+
+QH_OK, QH_EINVAL, QH_ERANGE, QH_EIO, QH_EFORMAT, QH_ENOMEM, QH_ESTATE = 0, -1, -2, -3, -4, -5, -6
+
+
+class QHError(RuntimeError):
+    def __init__(self, status: int, what: str = ""):
+        self.status = status
+        msg = _lib().qh_strerror(status).decode() if _LIB is not None else str(status)
+        super().__init__(f"{what}: status {status} ({msg})" if what else f"status {status} ({msg})")
+
+
+class Tensor(ctypes.Structure):
+    """qwen::Tensor (hls/src/types.hpp:51-56): int8 payload + per-row scales, or fp32."""
+
+    _fields_ = [
+        ("w_i8", ctypes.c_void_p),
+        ("scale", ctypes.c_void_p),
+        ("w_f32", ctypes.c_void_p),
+        ("out", ctypes.c_int),
+        ("in_", ctypes.c_int),
+    ]
+
+    @staticmethod
+    def i8(w, scale) -> "Tensor":
+        out, inn = int(w.shape[0]), int(w.shape[1])
+        return Tensor(_ptr(w), _ptr(scale), None, out, inn)
+
+    @staticmethod
+    def f32(w) -> "Tensor":
+        out, inn = int(w.shape[0]), int(w.shape[1])
+        return Tensor(None, None, _ptr(w), out, inn)
+
+
+_LIB: Optional[ctypes.CDLL] = None
+
+
+def library_path() -> str:
+    return LIB_PATH
+
+
+def _lib() -> ctypes.CDLL:
+    """Load libqh.so (built by __graft_entry__.build()); fail loudly if absent."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() first")
+        lib = ctypes.CDLL(LIB_PATH)
+        lib.qh_strerror.restype = ctypes.c_char_p
+        lib.qh_blob_size.restype = ctypes.c_size_t
+        lib.qh_layout_idx_text.restype = ctypes.c_size_t
+        lib.qh_layout_idx_text.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
+        lib.qh_synth_blob.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint64]
+        for n in ("qh_synth_fill_uniform", "qh_synth_fill_normal"):
+            getattr(lib, n).argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_float,
+                                        ctypes.c_float]
+        lib.qh_synth_fill_i8.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint64]
+        lib.qh_engine_device_ptr.restype = ctypes.c_void_p
+        lib.qh_engine_device_ptr.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        _LIB = lib
+    return _LIB
+
+
+def header_functions() -> list:
+    """Names of every function the C ABI header declares."""
+    text = open(HEADER_PATH).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qh_[a-z0-9_]+)\s*\(", text)))
+
+
+def _ptr(t) -> Optional[int]:
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    if hasattr(t, "data_ptr"):
+        return t.data_ptr()
+    if isinstance(t, np.ndarray):
+        return t.ctypes.data
+    raise TypeError(f"cannot pass {type(t)} as a pointer")
+
+
+def _stream(stream) -> Optional[int]:
+    if stream is None:
+        try:
+            import torch
+            return torch.cuda.current_stream().cuda_stream or None
+        except Exception:
+            return None
+    return getattr(stream, "cuda_stream", stream)
+
+
+def _check(status: int, what: str) -> None:
+    if status != QH_OK:
+        raise QHError(status, what)
+
+
+class _Ptr(int):
+    """An already-resolved raw pointer (e.g. a stream handle); 0 means NULL."""
+
+    def __new__(cls, v):
+        return int.__new__(cls, v or 0)
+
+
+def _call(name: str, *args) -> None:
+    """Call a C ABI function: ints -> int, floats -> float, Tensor -> struct
+    pointer, torch/numpy arrays -> data pointer, None -> NULL."""
+    fn = getattr(_lib(), name)
+    conv = []
+    for a in args:
+        if isinstance(a, _Ptr):
+            conv.append(ctypes.c_void_p(int(a)) if int(a) else None)
+        elif a is None:
+            conv.append(None)
+        elif isinstance(a, float):
+            conv.append(ctypes.c_float(a))
+        elif isinstance(a, Tensor):
+            conv.append(ctypes.byref(a))
+        elif isinstance(a, (bool, np.bool_, int, np.integer)):
+            conv.append(ctypes.c_int(int(a)))
+        else:
+            conv.append(ctypes.c_void_p(_ptr(a)))
+    _check(fn(*conv), name)
+
+
+# ---------------------------------------------------------------- op level
+# Integer sizes are passed as plain ints; pointers must be torch CUDA tensors.
+
+def gemv_i8(y, w, scale, x, out: int, in_: int, stream=None):
+    _call("qh_gemv_i8", y, w, scale, x, out, in_, _Ptr(_stream(stream)))
+
+
+def gemv_f32(y, w, x, out: int, in_: int, stream=None):
+    _call("qh_gemv_f32", y, w, x, out, in_, _Ptr(_stream(stream)))
+
+
+def row_dot_i8(result, w, scale, h, row: int, in_: int, stream=None):
+    _call("qh_row_dot_i8", result, w, scale, h, row, in_, _Ptr(_stream(stream)))
+
+
+def embed_row(h, w, scale, tok: int, in_: int, stream=None):
+    _call("qh_embed_row", h, w, scale, tok, in_, _Ptr(_stream(stream)))
+
+
+def rmsnorm(y, x, w, n: int, eps: float = EPS, stream=None):
+    _call("qh_rmsnorm", y, x, w, n, float(eps), _Ptr(_stream(stream)))
+
+
+def rmsnorm_gated(y, x, w, z, n: int, eps: float = EPS, stream=None):
+    _call("qh_rmsnorm_gated", y, x, w, z, n, float(eps), _Ptr(_stream(stream)))
+
+
+def conv1d_step(out, in_ch, state, weight, stream=None):
+    _call("qh_conv1d_step", out, in_ch, state, weight, _Ptr(_stream(stream)))
+
+
+def rope_cos_sin(pos: int, cos_o, sin_o, stream=None):
+    _call("qh_rope_cos_sin", pos, cos_o, sin_o, _Ptr(_stream(stream)))
+
+
+def apply_rope(x, cos_, sin_, stream=None):
+    _call("qh_apply_rope", x, cos_, sin_, _Ptr(_stream(stream)))
+
+
+def l2norm(v, n: int, stream=None):
+    _call("qh_l2norm", v, n, _Ptr(_stream(stream)))
+
+
+def delta_rule_head(q, k, v, g: float, beta: float, S, out, stream=None):
+    _call("qh_delta_rule_head", q, k, v, float(g), float(beta), S, out, _Ptr(_stream(stream)))
+
+
+def delta_rule_layer(q, k, v, g, beta, S, out, stream=None):
+    _call("qh_delta_rule_layer", q, k, v, g, beta, S, out, _Ptr(_stream(stream)))
+
+
+def deltanet_layer(out, x, qkv_w: Tensor, z_w: Tensor, b_w: Tensor, a_w: Tensor, conv_w, A_log, dt_bias,
+                   gate_norm_w, out_w: Tensor, rec, conv_state, w8a8: bool = False, stream=None):
+    _call("qh_deltanet_layer_w8a8" if w8a8 else "qh_deltanet_layer", out, x, qkv_w, z_w, b_w, a_w, conv_w,
+          A_log, dt_bias, gate_norm_w, out_w, rec, conv_state, _Ptr(_stream(stream)))
+
+
+def attention_layer(out, x, q_w: Tensor, k_w: Tensor, v_w: Tensor, o_w: Tensor, q_norm, k_norm, pos: int,
+                    kcache, vcache, T: int, w8a8: bool = False, stream=None):
+    _call("qh_attention_layer_w8a8" if w8a8 else "qh_attention_layer", out, x, q_w, k_w, v_w, o_w, q_norm,
+          k_norm, pos, kcache, vcache, T, _Ptr(_stream(stream)))
+
+
+def mlp_layer(out, x, gate_w: Tensor, up_w: Tensor, down_w: Tensor, w8a8: bool = False, stream=None):
+    _call("qh_mlp_layer_w8a8" if w8a8 else "qh_mlp_layer", out, x, gate_w, up_w, down_w,
+          _Ptr(_stream(stream)))
+
+
+def quant_act(xq, sx, x, n: int, stream=None):
+    _call("qh_quant_act", xq, sx, x, n, _Ptr(_stream(stream)))
+
+
+def gemv_i8_w8a8(y, acc, w, scale, xq, sx, out: int, in_: int, stream=None):
+    _call("qh_gemv_i8_w8a8", y, acc, w, scale, xq, sx, out, in_, _Ptr(_stream(stream)))
+
+
+# ---------------------------------------------------------------- layout / synthetic weights
+
+def blob_size() -> int:
+    return int(_lib().qh_blob_size())
+
+
+def idx_text() -> str:
+    lib = _lib()
+    n = lib.qh_layout_idx_text(None, 0)
+    buf = ctypes.create_string_buffer(n + 1)
+    lib.qh_layout_idx_text(buf, n + 1)
+    return buf.value.decode()
+
+
+def synth_blob(seed: int) -> np.ndarray:
+    """The seeded synthetic model in the packed pack_weights.py layout (host bytes)."""
+    n = blob_size()
+    blob = np.empty(n, dtype=np.uint8)
+    _check(_lib().qh_synth_blob(blob.ctypes.data, n, ctypes.c_uint64(seed)), "qh_synth_blob")
+    return blob
+
+
+def synth_i8(n: int, key: int) -> np.ndarray:
+    a = np.empty(n, dtype=np.int8)
+    _check(_lib().qh_synth_fill_i8(a.ctypes.data, n, ctypes.c_uint64(key)), "qh_synth_fill_i8")
+    return a
+
+
+def synth_uniform(n: int, key: int, lo: float, hi: float) -> np.ndarray:
+    a = np.empty(n, dtype=np.float32)
+    _check(_lib().qh_synth_fill_uniform(a.ctypes.data, n, ctypes.c_uint64(key), lo, hi), "fill_uniform")
+    return a
+
+
+def synth_normal(n: int, key: int, mean: float, std: float) -> np.ndarray:
+    a = np.empty(n, dtype=np.float32)
+    _check(_lib().qh_synth_fill_normal(a.ctypes.data, n, ctypes.c_uint64(key), mean, std), "fill_normal")
+    return a
+
+
+@dataclass
+class Entry:
+    """One weights.idx line (emit_weight_index.py:13-22)."""
+    name: str
+    off: int
+    nbytes: int
+    dtype: int
+    soff: int
+    snbytes: int
+    out: int
+    in_: int
+
+
+def parse_idx(text: str) -> dict:
+    ents = {}
+    for line in text.splitlines():
+        f = line.split()
+        if len(f) != 8:
+            continue
+        ents[f[0]] = Entry(f[0], int(f[1]), int(f[2]), int(f[3]), int(f[4]), int(f[5]), int(f[6]), int(f[7]))
+    return ents
+
+
+# ---------------------------------------------------------------- engine (qwen_top)
+
+class Engine:
+    """The decode top on the device: embed -> 24 layers -> final norm -> tied head.
+
+    Mirrors ``qwen_top(blob, state, tok, logits)`` (hls/src/qwen_synth.hpp:39-92)
+    with the ``DecodeState`` (hls/src/state.hpp:18-35) owned by the engine.
+    """
+
+    def __init__(self, blob=None, *, path: Optional[str] = None, idx: Optional[str] = None,
+                 max_ctx: int = 1024, mode: int = MODE_W8A16):
+        lib = _lib()
+        h = ctypes.c_void_p()
+        if path is not None:
+            st = lib.qh_engine_create(path.encode(), idx.encode() if idx else None, ctypes.c_int(max_ctx),
+                                      ctypes.byref(h))
+        else:
+            arr = np.ascontiguousarray(blob, dtype=np.uint8)
+            st = lib.qh_engine_create_from_memory(ctypes.c_void_p(arr.ctypes.data), ctypes.c_size_t(arr.size),
+                                                  idx.encode() if idx else None, ctypes.c_int(max_ctx),
+                                                  ctypes.byref(h))
+        _check(st, "qh_engine_create")
+        self._h = h
+        self.max_ctx = max_ctx
+        self.set_mode(mode)
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _lib().qh_engine_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def set_mode(self, mode: int):
+        _check(_lib().qh_engine_set_mode(self._h, ctypes.c_int(mode)), "qh_engine_set_mode")
+        self.mode = mode
+
+    def reset(self):
+        _check(_lib().qh_engine_reset(self._h), "qh_engine_reset")
+
+    @property
+    def pos(self) -> int:
+        return int(_lib().qh_engine_pos(self._h))
+
+    def decode_token(self, tok: int, want_logits: bool = False):
+        """qwen_top: returns (argmax, logits or None)."""
+        am = ctypes.c_int()
+        logits = np.empty(VOCAB, dtype=np.float32) if want_logits else None
+        _check(_lib().qh_decode_token(self._h, ctypes.c_int(tok),
+                                      ctypes.c_void_p(logits.ctypes.data) if want_logits else None,
+                                      ctypes.byref(am)), "qh_decode_token")
+        return int(am.value), logits
+
+    def generate(self, prompt: Sequence[int], n_new: int, eos: int = -1) -> list:
+        """The run_hls loop (run_hls.cpp:56-66), token feedback on the device."""
+        p = np.ascontiguousarray(np.asarray(prompt, dtype=np.int32))
+        out = np.empty(max(n_new, 1), dtype=np.int32)
+        n = ctypes.c_int()
+        _check(_lib().qh_generate(self._h, ctypes.c_void_p(p.ctypes.data), ctypes.c_int(p.size),
+                                  ctypes.c_int(n_new), ctypes.c_int(eos), ctypes.c_void_p(out.ctypes.data),
+                                  ctypes.byref(n)), "qh_generate")
+        return out[: n.value].tolist()
+
+    def forward_layers(self, l0: int, l1: int, h) -> None:
+        """Layers [l0, l1) on a device hidden vector h (torch, in place)."""
+        _check(_lib().qh_engine_forward_layers(self._h, ctypes.c_int(l0), ctypes.c_int(l1),
+                                               ctypes.c_void_p(_ptr(h))), "qh_engine_forward_layers")
+
+    def device_ptr(self, which: int) -> int:
+        return int(_lib().qh_engine_device_ptr(self._h, ctypes.c_int(which)) or 0)
+
+    @property
+    def last_argmax(self) -> int:
+        return int(_lib().qh_engine_last_argmax(self._h))

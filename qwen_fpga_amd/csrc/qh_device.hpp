@@ -1,0 +1,145 @@
+// Device helpers for the gfx950 decode kernels: deterministic transcendentals
+// and the fixed-order wavefront reductions every kernel uses.
+//
+// Determinism contract.  Every floating-point value the kernels produce is a
+// fixed sequence of IEEE-754 operations (round-to-nearest +, -, *, /, sqrt,
+// fma), independent of launch geometry and timing: no float atomics, fixed
+// reduction trees, and exp / log1p built here from those operations only.  The
+// code is compiled with -ffp-contract=off, so an fma appears exactly where
+// fmaf() is written.
+//
+// "C16" order for a length-n dot product or sum of squares: element i is in
+// chunk i/16, chunk c is owned by lane c mod 64, each lane accumulates its
+// elements in increasing i with fma starting from 0, and the L lane partials
+// (L = min(64, pow2ceil(ceil(n/16)))) are combined by the xor butterfly with
+// offsets L/2, ..., 1.  Since IEEE addition is commutative, every lane of a
+// butterfly group ends with the same, fully determined value.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qh {
+
+// exp: n = rint(x*log2 e); r = x - n*ln2 with a two-part ln2 (Cody-Waite);
+// e^r by its degree-7 Taylor polynomial (Horner, fma) on |r| <= ln2/2; exact
+// scaling by 2^n in at most two steps (overflow -> inf, deep underflow -> 0).
+__device__ __forceinline__ float dev_expf(float x) {
+  if (x != x) return x;
+  if (x > 88.72283935546875f) return __builtin_inff();
+  if (x < -103.972084045410156f) return 0.0f;
+  const float n = __builtin_rintf(x * 1.44269502162933349609375f);
+  float r = __builtin_fmaf(n, -0.693145751953125f, x);
+  r = __builtin_fmaf(n, -1.428606765330187045e-06f, r);
+  float p = 1.984126984126984e-4f;
+  p = __builtin_fmaf(p, r, 1.388888888888889e-3f);
+  p = __builtin_fmaf(p, r, 8.333333333333333e-3f);
+  p = __builtin_fmaf(p, r, 4.166666666666667e-2f);
+  p = __builtin_fmaf(p, r, 1.666666666666667e-1f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  int ni = (int)n;
+  if (ni > 127) { p = p * 2.0f; ni -= 1; }
+  if (ni < -126) { p = p * 5.42101086242752217e-20f; ni += 64; }
+  return p * __uint_as_float((uint32_t)(ni + 127) << 23);
+}
+
+// log for u >= 1: u = m*2^e, m in [sqrt(1/2), sqrt(2)); log m = 2*atanh(s),
+// s = (m-1)/(m+1), odd series to s^11; e*ln2 added with the two-part ln2.
+__device__ __forceinline__ float dev_logf_ge1(float u) {
+  const uint32_t b = __float_as_uint(u);
+  int e = (int)((b >> 23) & 0xffu) - 127;
+  float m = __uint_as_float((b & 0x007fffffu) | 0x3f800000u);
+  if (m > 1.41421353816986083984375f) { m = m * 0.5f; e += 1; }
+  const float s = (m - 1.0f) / (m + 1.0f);
+  const float s2 = s * s;
+  float t = 9.090909090909091e-2f;
+  t = __builtin_fmaf(t, s2, 1.111111111111111e-1f);
+  t = __builtin_fmaf(t, s2, 1.428571428571429e-1f);
+  t = __builtin_fmaf(t, s2, 2.0e-1f);
+  t = __builtin_fmaf(t, s2, 3.333333333333333e-1f);
+  t = __builtin_fmaf(t, s2, 1.0f);
+  const float lm = (2.0f * s) * t;
+  const float fe = (float)e;
+  return __builtin_fmaf(fe, 0.693145751953125f, __builtin_fmaf(fe, 1.428606765330187045e-06f, lm));
+}
+
+// log1p for y >= 0 (Goldberg: log(1+y) * y / ((1+y) - 1)).
+__device__ __forceinline__ float dev_log1pf(float y) {
+  if (y != y) return y;
+  if (y == __builtin_inff()) return y;
+  if (y < 1e-4f) return __builtin_fmaf(-0.5f * y, y, y);
+  const float u = 1.0f + y;
+  return dev_logf_ge1(u) * (y / (u - 1.0f));
+}
+
+// hls/src/activations.hpp:7-14 with the device exp / log1p.
+__device__ __forceinline__ float dev_silu(float x) { return x / (1.0f + dev_expf(-x)); }
+__device__ __forceinline__ float dev_sigmoid(float x) { return 1.0f / (1.0f + dev_expf(-x)); }
+__device__ __forceinline__ float dev_softplus(float x) {
+  return x > 20.0f ? x : dev_log1pf(dev_expf(x));
+}
+
+// xor butterfly over groups of WIDTH lanes (offsets WIDTH/2 .. 1).
+template <int WIDTH>
+__device__ __forceinline__ float xor_sum(float v) {
+#pragma unroll
+  for (int off = WIDTH / 2; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
+  return v;
+}
+template <int WIDTH>
+__device__ __forceinline__ int xor_sum_i(int v) {
+#pragma unroll
+  for (int off = WIDTH / 2; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
+  return v;
+}
+template <int WIDTH>
+__device__ __forceinline__ float xor_max(float v) {
+#pragma unroll
+  for (int off = WIDTH / 2; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Lane partial of a C16 dot over one 16-element chunk (fma, increasing index).
+__device__ __forceinline__ float dot16_f32(const float* a, const float* b, float acc) {
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc = __builtin_fmaf(a[e], b[e], acc);
+  return acc;
+}
+
+// int8 weights packed in 4 dwords (byte b of dword d = element 4d+b) times fp32.
+__device__ __forceinline__ float dot16_i8f(const uint32_t w[4], const float* x, float acc) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const float wf = (float)(int)(int8_t)(w[d] >> (8 * b));
+      acc = __builtin_fmaf(wf, x[4 * d + b], acc);
+    }
+  }
+  return acc;
+}
+
+// int8 x int8 -> int32 over 16 elements (v_dot4 on gfx950).
+__device__ __forceinline__ int dot16_i8i8(const uint32_t w[4], const uint32_t x[4], int acc) {
+  acc = __builtin_amdgcn_sdot4((int)w[0], (int)x[0], acc, false);
+  acc = __builtin_amdgcn_sdot4((int)w[1], (int)x[1], acc, false);
+  acc = __builtin_amdgcn_sdot4((int)w[2], (int)x[2], acc, false);
+  acc = __builtin_amdgcn_sdot4((int)w[3], (int)x[3], acc, false);
+  return acc;
+}
+
+// Per-vector symmetric int8 (golden/model.py:37-45 _qa): s = amax/127 (1 if
+// amax == 0), q = rint(x/s) clipped to +-127.
+__device__ __forceinline__ float quant_scale(float amax) { return amax > 0.0f ? amax / 127.0f : 1.0f; }
+__device__ __forceinline__ int quant_one(float x, float s) {
+  float r = __builtin_rintf(x / s);
+  r = fminf(fmaxf(r, -127.0f), 127.0f);
+  return (int)r;
+}
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+         ((uint32_t)(d & 0xff) << 24);
+}
+
+}  // namespace qh

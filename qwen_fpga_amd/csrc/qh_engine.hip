@@ -1,0 +1,519 @@
+// The decode engine: replaces the HLS decode top (hls/src/qwen_synth.hpp:39-92
+// qwen_top, hls/src/decoder.hpp:62-120 decode_token) and the DecodeState
+// (hls/src/state.hpp:18-35) with device-resident buffers.  One decode step is
+// recorded once as a hipGraph and replayed; the token, position and stop flag
+// live in a device StepCtl, so greedy generation runs without host round trips.
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "qh_common.hpp"
+#include "qh_kernels.hpp"
+#include "qh_layout.hpp"
+
+using namespace qh;
+
+struct qh_engine {
+  hipStream_t stream = nullptr;
+  const Layout* L = nullptr;
+  uint8_t* blob = nullptr;   // device copy of the packed weights
+  int max_ctx = 0;
+  int mode = M_W8A16;
+  // DecodeState (state.hpp:18-35)
+  float* rec = nullptr;    // [18][16][128][128]
+  float* conv = nullptr;   // [18][6144][4]
+  float* kc = nullptr;     // [6][max_ctx][512]
+  float* vc = nullptr;
+  // activations
+  float* h = nullptr;      // residual stream [1024]
+  float* convd = nullptr;  // [6144]
+  float* zb = nullptr;     // [2048]
+  float* gb = nullptr;     // g[16] beta[16]
+  float* o = nullptr;      // [2048]
+  float* act = nullptr;    // [3584]
+  float* og = nullptr;     // [2048]
+  float* qg = nullptr;     // [4096]
+  float* kraw = nullptr;   // [512]
+  float* vraw = nullptr;   // [512]
+  float* pm = nullptr;
+  float* pl = nullptr;
+  float* pacc = nullptr;
+  int nsplit_max = 0;
+  float* rope = nullptr;   // [max_ctx][64]
+  float* logits = nullptr; // [VOCAB]
+  float* part_val = nullptr;
+  int* part_idx = nullptr;
+  int head_grid = 0;
+  StepCtl* ctl = nullptr;
+  int* prompt_dev = nullptr;
+  int* out_dev = nullptr;
+  int io_cap = 0;
+  int host_pos = 0;
+  int last_argmax = -1;
+  // graphs[mode][logits][advance]
+  hipGraphExec_t graphs[2][2][2] = {};
+};
+
+namespace {
+
+const float* f32p(const qh_engine* e, int layer, Role r) {
+  const Entry* en = e->L->get(layer, r);
+  return reinterpret_cast<const float*>(e->blob + en->off);
+}
+const int8_t* i8p(const qh_engine* e, int layer, Role r) {
+  return reinterpret_cast<const int8_t*>(e->blob + e->L->get(layer, r)->off);
+}
+const float* scp(const qh_engine* e, int layer, Role r) {
+  return reinterpret_cast<const float*>(e->blob + e->L->get(layer, r)->soff);
+}
+
+Seg mkseg(int kind, int epi, int rows, int batch0, float* out) {
+  Seg g;
+  g.kind = kind;
+  g.epi = epi;
+  g.rows = rows;
+  g.batch0 = batch0;
+  g.nbatch = (rows + kRowsPerBatch - 1) / kRowsPerBatch;
+  g.out = out;
+  return g;
+}
+
+// Enqueue layers [l0, l1) of one decode step on the residual stream e->h.
+int enqueue_layers(qh_engine* e, int l0, int l1, bool embed, hipStream_t s) {
+  const int* done = &e->ctl->done;
+  int li = 0, fi = 0;
+  for (int l = 0; l < l0; ++l) (is_linear(l) ? li : fi)++;
+  for (int l = l0; l < l1; ++l) {
+    if (is_linear(l)) {
+      // in_ln rmsnorm (+ act-quant) -> qkv(conv+SiLU) | z | beta | g   (deltanet.hpp:149-165)
+      GemvArgs a;
+      a.K = kHidden;
+      a.mode = e->mode;
+      a.prologue = P_NORM;
+      a.x = e->h;
+      a.nw = f32p(e, l, R_IN_LN);
+      a.eps = kEps;
+      a.done = done;
+      if (embed && l == l0) {   // embed_row (qwen_synth.hpp:42-43), written to the residual
+        a.emb = i8p(e, kLayers, R_EMBED);
+        a.emb_s = scp(e, kLayers, R_EMBED);
+        a.tok = &e->ctl->tok;
+        a.h_out = e->h;
+      }
+      a.nseg = 4;
+      a.seg[0] = mkseg(SEG_I8, E_CONV, kConvDim, 0, e->convd);
+      a.seg[0].w = i8p(e, l, R_QKV);
+      a.seg[0].sw = scp(e, l, R_QKV);
+      a.seg[0].c0 = f32p(e, l, R_CONV);
+      a.seg[0].c2 = e->conv + (size_t)li * kConvDim * kConvK;
+      a.seg[1] = mkseg(SEG_I8, E_STORE, kZDim, a.seg[0].nbatch, e->zb);
+      a.seg[1].w = i8p(e, l, R_Z);
+      a.seg[1].sw = scp(e, l, R_Z);
+      a.seg[2] = mkseg(SEG_F32, E_GATE_B, kLH, a.seg[1].batch0 + a.seg[1].nbatch, e->gb + 16);
+      a.seg[2].wf = f32p(e, l, R_B);
+      a.seg[3] = mkseg(SEG_F32, E_GATE_A, kLH, a.seg[2].batch0 + a.seg[2].nbatch, e->gb);
+      a.seg[3].wf = f32p(e, l, R_A);
+      a.seg[3].c0 = f32p(e, l, R_ALOG);
+      a.seg[3].c1 = f32p(e, l, R_DTB);
+      QH_HIP(launch_gemv(a, 4, s));
+      DnArgs d;   // l2norm, delta rule (deltanet.hpp:166-173)
+      d.convd = e->convd;
+      d.gb = e->gb;
+      d.S = e->rec + (size_t)li * kLH * kLK * kLV;
+      d.o = e->o;
+      d.done = done;
+      QH_HIP(launch_deltanet(d, s));
+      GemvArgs c;   // gated rmsnorm (+ quant) -> out_proj, residual add (deltanet.hpp:177-181)
+      c.K = kLH * kLV;
+      c.mode = e->mode;
+      c.prologue = P_GATED;
+      c.x = e->o;
+      c.nw = f32p(e, l, R_LNORM);
+      c.z = e->zb;
+      c.eps = kEps;
+      c.done = done;
+      c.nseg = 1;
+      c.seg[0] = mkseg(SEG_I8, E_RESID, kHidden, 0, e->h);
+      c.seg[0].w = i8p(e, l, R_OUTP);
+      c.seg[0].sw = scp(e, l, R_OUTP);
+      QH_HIP(launch_gemv(c, 1, s));
+      ++li;
+    } else {
+      GemvArgs a;   // in_ln rmsnorm (+ quant) -> q||gate, k, v (attention.hpp:31-33)
+      a.K = kHidden;
+      a.mode = e->mode;
+      a.prologue = P_NORM;
+      a.x = e->h;
+      a.nw = f32p(e, l, R_IN_LN);
+      a.eps = kEps;
+      a.done = done;
+      a.nseg = 3;
+      a.seg[0] = mkseg(SEG_I8, E_STORE, kQProj, 0, e->qg);
+      a.seg[0].w = i8p(e, l, R_QP);
+      a.seg[0].sw = scp(e, l, R_QP);
+      a.seg[1] = mkseg(SEG_I8, E_STORE, kKVProj, a.seg[0].nbatch, e->kraw);
+      a.seg[1].w = i8p(e, l, R_KP);
+      a.seg[1].sw = scp(e, l, R_KP);
+      a.seg[2] = mkseg(SEG_I8, E_STORE, kKVProj, a.seg[1].batch0 + a.seg[1].nbatch, e->vraw);
+      a.seg[2].w = i8p(e, l, R_VP);
+      a.seg[2].sw = scp(e, l, R_VP);
+      QH_HIP(launch_gemv(a, 4, s));
+      AttnArgs at;
+      at.qg = e->qg;
+      at.kraw = e->kraw;
+      at.vraw = e->vraw;
+      at.qn = f32p(e, l, R_QN);
+      at.kn = f32p(e, l, R_KN);
+      at.rope = e->rope;
+      at.kc = e->kc + (size_t)fi * e->max_ctx * kKVProj;
+      at.vc = e->vc + (size_t)fi * e->max_ctx * kKVProj;
+      at.T = &e->ctl->pos;
+      at.rope_row = &e->ctl->pos;
+      at.pm = e->pm;
+      at.pl = e->pl;
+      at.pacc = e->pacc;
+      at.nsplit_max = e->nsplit_max;
+      at.max_ctx = e->max_ctx;
+      at.og = e->og;
+      at.eps = kEps;
+      at.done = done;
+      QH_HIP(launch_attn(at, s));
+      QH_HIP(launch_attn_combine(at, s));
+      GemvArgs c;   // (+ quant) o_proj, residual add (attention.hpp:94)
+      c.K = kNH * kHD;
+      c.mode = e->mode;
+      c.prologue = P_LOAD;
+      c.x = e->og;
+      c.done = done;
+      c.nseg = 1;
+      c.seg[0] = mkseg(SEG_I8, E_RESID, kHidden, 0, e->h);
+      c.seg[0].w = i8p(e, l, R_OP);
+      c.seg[0].sw = scp(e, l, R_OP);
+      QH_HIP(launch_gemv(c, 1, s));
+      ++fi;
+    }
+    // post_ln rmsnorm (+ quant) -> gate||up pairs with SwiGLU -> down, residual (mlp.hpp:11-19)
+    GemvArgs m;
+    m.K = kHidden;
+    m.mode = e->mode;
+    m.prologue = P_NORM;
+    m.x = e->h;
+    m.nw = f32p(e, l, R_POST_LN);
+    m.eps = kEps;
+    m.done = done;
+    m.nseg = 1;
+    m.seg[0] = mkseg(SEG_PAIR, E_SWIGLU, 2 * kInter, 0, e->act);
+    m.seg[0].w = i8p(e, l, R_GATE);
+    m.seg[0].sw = scp(e, l, R_GATE);
+    m.seg[0].w2 = i8p(e, l, R_UP);
+    m.seg[0].sw2 = scp(e, l, R_UP);
+    QH_HIP(launch_gemv(m, 4, s));
+    GemvArgs dn;
+    dn.K = kInter;
+    dn.mode = e->mode;
+    dn.prologue = P_LOAD;
+    dn.x = e->act;
+    dn.done = done;
+    dn.nseg = 1;
+    dn.seg[0] = mkseg(SEG_I8, E_RESID, kHidden, 0, e->h);
+    dn.seg[0].w = i8p(e, l, R_DOWN);
+    dn.seg[0].sw = scp(e, l, R_DOWN);
+    QH_HIP(launch_gemv(dn, 1, s));
+  }
+  return QH_OK;
+}
+
+// One full decode step (qwen_top): embed, 24 layers, final norm, tied head,
+// argmax (+ pos), optionally the generation bookkeeping.
+int enqueue_step(qh_engine* e, bool with_logits, bool advance, hipStream_t s) {
+  QH_TRY(enqueue_layers(e, 0, kLayers, true, s));
+  HeadArgs hd;
+  hd.h = e->h;
+  hd.nw = f32p(e, kLayers, R_FINAL);
+  hd.eps = kEps;
+  hd.w = i8p(e, kLayers, R_EMBED);
+  hd.sw = scp(e, kLayers, R_EMBED);
+  hd.rows = kVocab;
+  hd.logits = with_logits ? e->logits : nullptr;
+  hd.part_val = e->part_val;
+  hd.part_idx = e->part_idx;
+  hd.done = &e->ctl->done;
+  QH_HIP(launch_head(hd, e->head_grid, s));
+  QH_HIP(launch_argmax(e->part_val, e->part_idx, e->head_grid, e->ctl, nullptr, s));
+  if (advance) QH_HIP(launch_advance(e->ctl, e->prompt_dev, e->out_dev, s));
+  return QH_OK;
+}
+
+int get_graph(qh_engine* e, bool with_logits, bool advance, hipGraphExec_t* out) {
+  hipGraphExec_t& ge = e->graphs[e->mode][with_logits][advance];
+  if (ge == nullptr) {
+    hipGraph_t g = nullptr;
+    QH_HIP(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+    const int st = enqueue_step(e, with_logits, advance, e->stream);
+    const hipError_t ec = hipStreamEndCapture(e->stream, &g);
+    if (st != QH_OK) {
+      if (g) (void)hipGraphDestroy(g);
+      return st;
+    }
+    QH_HIP(ec);
+    const hipError_t ei = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    QH_HIP(ei);
+  }
+  *out = ge;
+  return QH_OK;
+}
+
+template <class T>
+int dalloc(T** p, size_t n) {
+  return hip_status(hipMalloc(reinterpret_cast<void**>(p), n * sizeof(T)));
+}
+
+void release(qh_engine* e) {
+  if (!e) return;
+  if (e->stream) (void)hipStreamSynchronize(e->stream);
+  for (auto& a : e->graphs)
+    for (auto& b : a)
+      for (auto& g : b)
+        if (g) (void)hipGraphExecDestroy(g);
+  void* bufs[] = {e->blob, e->rec, e->conv, e->kc, e->vc, e->h, e->convd, e->zb, e->gb, e->o, e->act,
+                  e->og, e->qg, e->kraw, e->vraw, e->pm, e->pl, e->pacc, e->rope, e->logits, e->part_val,
+                  e->part_idx, e->ctl, e->prompt_dev, e->out_dev};
+  for (void* p : bufs)
+    if (p) (void)hipFree(p);
+  if (e->stream) (void)hipStreamDestroy(e->stream);
+  delete e;
+}
+
+int ensure_io(qh_engine* e, int n) {
+  if (n <= e->io_cap) return QH_OK;
+  if (e->prompt_dev) (void)hipFree(e->prompt_dev);
+  if (e->out_dev) (void)hipFree(e->out_dev);
+  e->prompt_dev = e->out_dev = nullptr;
+  // the generation graphs bake these pointers in
+  for (auto& a : e->graphs)
+    for (auto& b : a)
+      if (b[1]) {
+        (void)hipGraphExecDestroy(b[1]);
+        b[1] = nullptr;
+      }
+  int cap = 1024;
+  while (cap < n) cap *= 2;
+  QH_TRY(dalloc(&e->prompt_dev, (size_t)cap));
+  QH_TRY(dalloc(&e->out_dev, (size_t)cap));
+  e->io_cap = cap;
+  return QH_OK;
+}
+
+int create(const void* blob, size_t blob_len, const char* idx_text, int max_ctx, qh_engine** out) {
+  if (!out) return QH_EINVAL;
+  *out = nullptr;
+  if (!blob || max_ctx < 1) return QH_EINVAL;
+  const Layout& L = canonical_layout();
+  if (blob_len != L.total) return QH_EFORMAT;
+  if (idx_text && !check_idx_text(idx_text, L).empty()) return QH_EFORMAT;
+  qh_engine* e = new (std::nothrow) qh_engine();
+  if (!e) return QH_ENOMEM;
+  e->L = &L;
+  e->max_ctx = max_ctx;
+  e->nsplit_max = (max_ctx + kAttnSplit - 1) / kAttnSplit;
+  e->head_grid = kVocab / (kRowsPerBatch * 4 * 4);   // 4 waves x 4 batches per block
+  int st = QH_OK;
+#define QH_C(expr)             \
+  do {                         \
+    st = (expr);               \
+    if (st != QH_OK) goto fail; \
+  } while (0)
+  QH_C(hip_status(hipStreamCreate(&e->stream)));
+  QH_C(dalloc(&e->blob, blob_len));
+  QH_C(hip_status(hipMemcpy(e->blob, blob, blob_len, hipMemcpyHostToDevice)));
+  QH_C(dalloc(&e->rec, (size_t)kNLinear * kLH * kLK * kLV));
+  QH_C(dalloc(&e->conv, (size_t)kNLinear * kConvDim * kConvK));
+  QH_C(dalloc(&e->kc, (size_t)kNFull * max_ctx * kKVProj));
+  QH_C(dalloc(&e->vc, (size_t)kNFull * max_ctx * kKVProj));
+  QH_C(dalloc(&e->h, kHidden));
+  QH_C(dalloc(&e->convd, kConvDim));
+  QH_C(dalloc(&e->zb, kZDim));
+  QH_C(dalloc(&e->gb, 32));
+  QH_C(dalloc(&e->o, kLH * kLV));
+  QH_C(dalloc(&e->act, kInter));
+  QH_C(dalloc(&e->og, kNH * kHD));
+  QH_C(dalloc(&e->qg, kQProj));
+  QH_C(dalloc(&e->kraw, kKVProj));
+  QH_C(dalloc(&e->vraw, kKVProj));
+  QH_C(dalloc(&e->pm, (size_t)8 * e->nsplit_max));
+  QH_C(dalloc(&e->pl, (size_t)8 * e->nsplit_max));
+  QH_C(dalloc(&e->pacc, (size_t)8 * e->nsplit_max * 256));
+  QH_C(dalloc(&e->rope, (size_t)max_ctx * 64));
+  QH_C(dalloc(&e->logits, kVocab));
+  QH_C(dalloc(&e->part_val, e->head_grid));
+  QH_C(dalloc(&e->part_idx, e->head_grid));
+  QH_C(dalloc(&e->ctl, 1));
+  {
+    std::vector<float> rope((size_t)max_ctx * 64);
+    for (int p = 0; p < max_ctx; ++p) rope_row(p, &rope[(size_t)p * 64]);
+    QH_C(hip_status(hipMemcpy(e->rope, rope.data(), rope.size() * 4, hipMemcpyHostToDevice)));
+  }
+  QH_C(ensure_io(e, 1024));
+  QH_C(qh_engine_reset(e));
+#undef QH_C
+  *out = e;
+  return QH_OK;
+fail:
+  release(e);
+  return st;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qh_engine_create_from_memory(const void* blob, size_t blob_len, const char* idx_text, int max_ctx,
+                                 qh_engine** out) {
+  return create(blob, blob_len, idx_text, max_ctx, out);
+}
+
+int qh_engine_create(const char* blob_path, const char* idx_path, int max_ctx, qh_engine** out) {
+  if (!blob_path || !out) return QH_EINVAL;
+  std::string idx;
+  if (idx_path) {   // tb_decode.cpp:47-51
+    std::ifstream f(idx_path);
+    if (!f) return QH_EIO;
+    std::stringstream ss;
+    ss << f.rdbuf();
+    idx = ss.str();
+  }
+  const int fd = ::open(blob_path, O_RDONLY);   // run_hls.cpp:27-35
+  if (fd < 0) return QH_EIO;
+  struct stat sb;
+  if (::fstat(fd, &sb) != 0) {
+    ::close(fd);
+    return QH_EIO;
+  }
+  const size_t len = (size_t)sb.st_size;
+  if (len != canonical_layout().total) {
+    ::close(fd);
+    return QH_EFORMAT;
+  }
+  void* p = ::mmap(nullptr, len, PROT_READ, MAP_PRIVATE, fd, 0);
+  ::close(fd);
+  if (p == MAP_FAILED) return QH_EIO;
+  const int st = create(p, len, idx_path ? idx.c_str() : nullptr, max_ctx, out);
+  ::munmap(p, len);
+  return st;
+}
+
+int qh_engine_destroy(qh_engine* e) {
+  if (!e) return QH_EINVAL;
+  release(e);
+  return QH_OK;
+}
+
+int qh_engine_set_mode(qh_engine* e, int mode) {
+  if (!e || (mode != QH_MODE_W8A16 && mode != QH_MODE_W8A8)) return QH_EINVAL;
+  e->mode = mode == QH_MODE_W8A8 ? M_W8A8 : M_W8A16;
+  return QH_OK;
+}
+
+int qh_engine_reset(qh_engine* e) {
+  if (!e) return QH_EINVAL;
+  hipStream_t s = e->stream;
+  QH_HIP(hipMemsetAsync(e->rec, 0, sizeof(float) * (size_t)kNLinear * kLH * kLK * kLV, s));
+  QH_HIP(hipMemsetAsync(e->conv, 0, sizeof(float) * (size_t)kNLinear * kConvDim * kConvK, s));
+  QH_HIP(hipMemsetAsync(e->kc, 0, sizeof(float) * (size_t)kNFull * e->max_ctx * kKVProj, s));
+  QH_HIP(hipMemsetAsync(e->vc, 0, sizeof(float) * (size_t)kNFull * e->max_ctx * kKVProj, s));
+  StepCtl c;
+  std::memset(&c, 0, sizeof c);
+  c.max_ctx = e->max_ctx;
+  c.eos = -1;
+  QH_HIP(hipMemcpyAsync(e->ctl, &c, sizeof c, hipMemcpyHostToDevice, s));
+  QH_HIP(hipStreamSynchronize(s));
+  e->host_pos = 0;
+  e->last_argmax = -1;
+  return QH_OK;
+}
+
+int qh_decode_token(qh_engine* e, int tok, float* logits, int* argmax_out) {
+  if (!e || !argmax_out) return QH_EINVAL;
+  if (tok < 0 || tok >= kVocab) return QH_ERANGE;
+  if (e->host_pos >= e->max_ctx) return QH_ERANGE;
+  hipGraphExec_t g;
+  QH_TRY(get_graph(e, logits != nullptr, false, &g));
+  hipStream_t s = e->stream;
+  QH_HIP(launch_set_int(&e->ctl->tok, tok, s));
+  QH_HIP(launch_set_int(&e->ctl->done, 0, s));
+  QH_HIP(hipGraphLaunch(g, s));
+  StepCtl c;
+  QH_HIP(hipMemcpyAsync(&c, e->ctl, sizeof c, hipMemcpyDeviceToHost, s));
+  if (logits) QH_HIP(hipMemcpyAsync(logits, e->logits, sizeof(float) * kVocab, hipMemcpyDeviceToHost, s));
+  QH_HIP(hipStreamSynchronize(s));
+  e->host_pos = c.pos;
+  e->last_argmax = c.argmax;
+  *argmax_out = c.argmax;
+  return QH_OK;
+}
+
+int qh_generate(qh_engine* e, const int* prompt, int n_prompt, int n_new, int eos, int* out_ids, int* n_out) {
+  if (!e || !prompt || n_prompt < 1 || n_new < 0 || (n_new > 0 && !out_ids) || !n_out) return QH_EINVAL;
+  for (int i = 0; i < n_prompt; ++i)
+    if (prompt[i] < 0 || prompt[i] >= kVocab) return QH_ERANGE;
+  if ((long)e->host_pos + n_prompt + n_new > e->max_ctx) return QH_ERANGE;
+  QH_TRY(ensure_io(e, n_prompt > n_new ? n_prompt : n_new));
+  hipStream_t s = e->stream;
+  QH_HIP(hipMemcpyAsync(e->prompt_dev, prompt, sizeof(int) * (size_t)n_prompt, hipMemcpyHostToDevice, s));
+  QH_HIP(hipStreamSynchronize(s));
+  hipGraphExec_t g;
+  QH_TRY(get_graph(e, false, true, &g));
+  QH_HIP(launch_init_gen(e->ctl, prompt[0], n_prompt, n_new, eos, s));
+  for (int i = 0; i < n_prompt + n_new; ++i) QH_HIP(hipGraphLaunch(g, s));
+  StepCtl c;
+  QH_HIP(hipMemcpyAsync(&c, e->ctl, sizeof c, hipMemcpyDeviceToHost, s));
+  QH_HIP(hipStreamSynchronize(s));
+  if (c.n_out > 0) QH_HIP(hipMemcpy(out_ids, e->out_dev, sizeof(int) * (size_t)c.n_out, hipMemcpyDeviceToHost));
+  *n_out = c.n_out;
+  e->host_pos = c.pos;
+  e->last_argmax = c.argmax;
+  QH_HIP(launch_set_int(&e->ctl->done, 0, s));
+  QH_HIP(hipStreamSynchronize(s));
+  return c.err == 2 ? QH_ERANGE : QH_OK;
+}
+
+int qh_engine_pos(const qh_engine* e) { return e ? e->host_pos : -1; }
+int qh_engine_last_argmax(const qh_engine* e) { return e ? e->last_argmax : -1; }
+
+int qh_engine_forward_layers(qh_engine* e, int l0, int l1, float* h) {
+  if (!e || !h || l0 < 0 || l1 > kLayers || l0 >= l1) return QH_EINVAL;
+  if (e->host_pos >= e->max_ctx) return QH_ERANGE;
+  hipStream_t s = e->stream;
+  QH_HIP(launch_set_int(&e->ctl->done, 0, s));
+  QH_HIP(hipMemcpyAsync(e->h, h, sizeof(float) * kHidden, hipMemcpyDeviceToDevice, s));
+  QH_TRY(enqueue_layers(e, l0, l1, false, s));
+  QH_HIP(launch_bump_pos(e->ctl, s));
+  QH_HIP(hipMemcpyAsync(h, e->h, sizeof(float) * kHidden, hipMemcpyDeviceToDevice, s));
+  QH_HIP(hipStreamSynchronize(s));
+  e->host_pos += 1;
+  return QH_OK;
+}
+
+void* qh_engine_device_ptr(qh_engine* e, int which) {
+  if (!e) return nullptr;
+  switch (which) {
+    case 0: return e->blob;
+    case 1: return e->rec;
+    case 2: return e->conv;
+    case 3: return e->kc;
+    case 4: return e->vc;
+    case 5: return e->h;
+    default: return nullptr;
+  }
+}
+
+}  // extern "C"

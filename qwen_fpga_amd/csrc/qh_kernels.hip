@@ -1,0 +1,897 @@
+// gfx950 kernels of the decode datapath.  Every reduction follows the fixed
+// orders documented in qh_device.hpp (C16 and the 8-row transposed butterfly),
+// so results do not depend on grid size or timing.
+#include "qh_device.hpp"
+#include "qh_kernels.hpp"
+
+namespace qh {
+
+// ===========================================================================
+// GEMV: y = W x over up to four row segments sharing one activation vector.
+// A wave owns batches of 8 rows; lane l holds the 16-element chunks
+// c = l + 64j of x in registers and streams the same chunks of each row with
+// one 16-byte load per chunk (a row of 1024 int8 is one coalesced 1 KiB read
+// across the wave).  After the lane partials, reduce8 folds the 8 rows with a
+// transposed xor butterfly: at offsets 32, 16, 8 each lane keeps half of its
+// rows and receives its partner's other half, then offsets 4, 2, 1 finish the
+// tree.  Lane l ends with row (l >> 3) & 7.  Per row this is exactly the
+// 64-lane xor tree of the C16 order.
+// ===========================================================================
+template <typename T>
+__device__ __forceinline__ T reduce8(T v[8], int lane) {
+  {
+    const bool up = (lane & 32) != 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const T send = up ? v[i] : v[i + 4];
+      const T keep = up ? v[i + 4] : v[i];
+      v[i] = keep + __shfl_xor(send, 32, 64);
+    }
+  }
+  {
+    const bool up = (lane & 16) != 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const T send = up ? v[i] : v[i + 2];
+      const T keep = up ? v[i + 2] : v[i];
+      v[i] = keep + __shfl_xor(send, 16, 64);
+    }
+  }
+  {
+    const bool up = (lane & 8) != 0;
+    const T send = up ? v[0] : v[1];
+    const T keep = up ? v[1] : v[0];
+    v[0] = keep + __shfl_xor(send, 8, 64);
+  }
+  T r = v[0];
+  r = r + __shfl_xor(r, 4, 64);
+  r = r + __shfl_xor(r, 2, 64);
+  r = r + __shfl_xor(r, 1, 64);
+  return r;
+}
+
+__device__ __forceinline__ void load16f(const float* p, float* v) {
+  const float4* q = reinterpret_cast<const float4*>(p);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float4 t = q[k];
+    v[4 * k + 0] = t.x;
+    v[4 * k + 1] = t.y;
+    v[4 * k + 2] = t.z;
+    v[4 * k + 3] = t.w;
+  }
+}
+__device__ __forceinline__ void store16f(float* p, const float* v) {
+  float4* q = reinterpret_cast<float4*>(p);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) q[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+}
+__device__ __forceinline__ void load16b(const int8_t* p, uint32_t* w) {
+  const uint4 t = *reinterpret_cast<const uint4*>(p);
+  w[0] = t.x;
+  w[1] = t.y;
+  w[2] = t.z;
+  w[3] = t.w;
+}
+__device__ __forceinline__ float i8_at(const uint32_t* w, int e) {
+  return (float)(int)(int8_t)(w[e >> 2] >> (8 * (e & 3)));
+}
+
+__device__ __forceinline__ const int8_t* seg_row(const Seg& g, int row, int K) {
+  if (g.kind == SEG_PAIR) return ((row & 1) ? g.w2 : g.w) + (size_t)(row >> 1) * K;
+  return g.w + (size_t)row * K;
+}
+__device__ __forceinline__ float seg_scale(const Seg& g, int row) {
+  if (g.kind == SEG_PAIR) return (row & 1) ? g.sw2[row >> 1] : g.sw[row >> 1];
+  return g.sw[row];
+}
+
+// Row-batch epilogue: lane l holds the result y of row (l >> 3) & 7 of the batch.
+__device__ __forceinline__ void gemv_epilogue(const Seg& g, int lane, int myrow, float y, int acci) {
+  if (g.epi == E_SWIGLU) {   // pair rows: even = gate i, odd = up i (mlp.hpp:17)
+    const float yo = __shfl_xor(y, 8, 64);
+    if ((lane & 15) == 0 && myrow < g.rows) g.out[myrow >> 1] = dev_silu(y) * yo;
+    return;
+  }
+  if ((lane & 7) != 0 || myrow >= g.rows) return;
+  switch (g.epi) {
+    case E_STORE:
+      g.out[myrow] = y;
+      break;
+    case E_RESID:
+      g.out[myrow] = g.out[myrow] + y;
+      break;
+    case E_ACC:
+      g.out[myrow] = y;
+      g.acc_out[myrow] = acci;
+      break;
+    case E_GATE_B:
+      g.out[myrow] = dev_sigmoid(y);
+      break;
+    case E_GATE_A:
+      g.out[myrow] = -dev_expf(g.c0[myrow]) * dev_softplus(y + g.c1[myrow]);
+      break;
+    case E_CONV: {   // conv1d.hpp:22-36
+      float* st = g.c2 + (size_t)myrow * 4;
+      const float* w = g.c0 + (size_t)myrow * 4;
+      const float w0 = st[1], w1 = st[2], w2 = st[3], w3 = y;
+      float acc = 0.0f;
+      acc = acc + w0 * w[0];
+      acc = acc + w1 * w[1];
+      acc = acc + w2 * w[2];
+      acc = acc + w3 * w[3];
+      st[0] = w0;
+      st[1] = w1;
+      st[2] = w2;
+      st[3] = w3;
+      g.out[myrow] = dev_silu(acc);
+      break;
+    }
+    default:
+      break;
+  }
+}
+
+template <int NCH, int MODE, int PRO>
+__global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
+  if (a.done != nullptr && *a.done != 0) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwv = blockDim.x >> 6;
+  const int K = a.K, nchunk = K >> 4;
+  float xv[NCH][16];     // fp32 activation (W8A16) / dequantized q*s (W8A8)
+  uint32_t xq[NCH][4];   // int8 activation (W8A8)
+  float xs = 1.0f;       // activation scale (W8A8)
+
+  // ---------------- prologue: this lane's chunks c = lane + 64 j of x
+  if constexpr (PRO == P_LOADQ) {
+    xs = *a.sx;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = lane + 64 * j;
+      if (c < nchunk) {
+        load16b(a.xq + 16 * c, xq[j]);
+      } else {
+        xq[j][0] = xq[j][1] = xq[j][2] = xq[j][3] = 0u;
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) xv[j][e] = i8_at(xq[j], e) * xs;
+    }
+  } else {
+    if (PRO == P_NORM && a.emb != nullptr) {   // embed_row (gemv.hpp:76-84)
+      const int tok = *a.tok;
+      const int8_t* er = a.emb + (size_t)tok * K;
+      const float es = a.emb_s[tok];
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int c = lane + 64 * j;
+        if (c < nchunk) {
+          uint32_t w[4];
+          load16b(er + 16 * c, w);
+#pragma unroll
+          for (int e = 0; e < 16; ++e) xv[j][e] = i8_at(w, e) * es;
+          if (a.h_out != nullptr && blockIdx.x == 0 && threadIdx.x < 64) store16f(a.h_out + 16 * c, xv[j]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) xv[j][e] = 0.0f;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int c = lane + 64 * j;
+        if (c < nchunk) {
+          load16f(a.x + 16 * c, xv[j]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) xv[j][e] = 0.0f;
+        }
+      }
+    }
+    if constexpr (PRO == P_NORM) {   // norm.hpp:13-20, sum of squares in C16 order
+      float ss = 0.0f;
+#pragma unroll
+      for (int j = 0; j < NCH; ++j)
+        if (lane + 64 * j < nchunk) ss = dot16_f32(xv[j], xv[j], ss);
+      ss = xor_sum<64>(ss);
+      const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int c = lane + 64 * j;
+        if (c < nchunk) {
+          float w[16];
+          load16f(a.nw + 16 * c, w);
+#pragma unroll
+          for (int e = 0; e < 16; ++e) xv[j][e] = (xv[j][e] * inv) * (1.0f + w[e]);
+        }
+      }
+    } else if constexpr (PRO == P_GATED) {   // heads of 128 = groups of 8 lanes
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int c = lane + 64 * j;
+        float ss = dot16_f32(xv[j], xv[j], 0.0f);
+        ss = xor_sum<8>(ss);
+        const float inv = 1.0f / sqrtf(ss / 128.0f + a.eps);
+        if (c < nchunk) {
+          float w[16], z[16];
+          load16f(a.nw + ((16 * c) & 127), w);
+          load16f(a.z + 16 * c, z);
+#pragma unroll
+          for (int e = 0; e < 16; ++e) xv[j][e] = ((xv[j][e] * inv) * w[e]) * dev_silu(z[e]);
+        }
+      }
+    }
+    if constexpr (MODE == M_W8A8) {   // _qa (golden/model.py:37-45)
+      float am = 0.0f;
+#pragma unroll
+      for (int j = 0; j < NCH; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) am = fmaxf(am, fabsf(xv[j][e]));
+      am = xor_max<64>(am);
+      xs = quant_scale(am);
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        int q[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          q[e] = quant_one(xv[j][e], xs);
+          xv[j][e] = (float)q[e] * xs;
+        }
+#pragma unroll
+        for (int d = 0; d < 4; ++d) xq[j][d] = pack4(q[4 * d], q[4 * d + 1], q[4 * d + 2], q[4 * d + 3]);
+      }
+    }
+  }
+
+  // ---------------- row batches
+  const int total = a.seg[a.nseg - 1].batch0 + a.seg[a.nseg - 1].nbatch;
+  for (int b = blockIdx.x * nwv + wave; b < total; b += gridDim.x * nwv) {
+    int si = 0;
+    while (si + 1 < a.nseg && b >= a.seg[si + 1].batch0) ++si;
+    const Seg& g = a.seg[si];
+    const int row0 = (b - g.batch0) * kRowsPerBatch;
+    const int myrow = row0 + ((lane >> 3) & 7);
+    float y = 0.0f;
+    int acci = 0;
+    if (g.kind == SEG_F32) {   // fp32 weights (gemv.hpp:46-59)
+      float p[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) p[r] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int c = lane + 64 * j;
+        if (c < nchunk) {
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            if (row0 + r < g.rows) {
+              float w[16];
+              load16f(g.wf + (size_t)(row0 + r) * K + 16 * c, w);
+              p[r] = dot16_f32(w, xv[j], p[r]);
+            }
+          }
+        }
+      }
+      y = reduce8(p, lane);
+    } else if constexpr (MODE == M_W8A16) {   // int8 x fp32 (gemv.hpp:28-42)
+      float p[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) p[r] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int c = lane + 64 * j;
+        if (c < nchunk) {
+          uint32_t w[8][4];
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            if (row0 + r < g.rows) {
+              load16b(seg_row(g, row0 + r, K) + 16 * c, w[r]);
+            } else {
+              w[r][0] = w[r][1] = w[r][2] = w[r][3] = 0u;
+            }
+          }
+#pragma unroll
+          for (int r = 0; r < 8; ++r) p[r] = dot16_i8f(w[r], xv[j], p[r]);
+        }
+      }
+      y = reduce8(p, lane);
+      if (myrow < g.rows) y = y * seg_scale(g, myrow);
+    } else {   // int8 x int8 -> int32, dequant float(acc)*sx*sw (export_gemv_tv.py:298-299)
+      int p[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) p[r] = 0;
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int c = lane + 64 * j;
+        if (c < nchunk) {
+          uint32_t w[8][4];
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            if (row0 + r < g.rows) {
+              load16b(seg_row(g, row0 + r, K) + 16 * c, w[r]);
+            } else {
+              w[r][0] = w[r][1] = w[r][2] = w[r][3] = 0u;
+            }
+          }
+#pragma unroll
+          for (int r = 0; r < 8; ++r) p[r] = dot16_i8i8(w[r], xq[j], p[r]);
+        }
+      }
+      acci = reduce8(p, lane);
+      if (myrow < g.rows) y = ((float)acci * xs) * seg_scale(g, myrow);
+    }
+    gemv_epilogue(g, lane, myrow, y, acci);
+  }
+}
+
+template <int NCH, int MODE>
+static void launch_gemv_pro(const GemvArgs& a, int grid, dim3 blk, hipStream_t s) {
+  switch (a.prologue) {
+    case P_NORM: gemv_kernel<NCH, MODE, P_NORM><<<grid, blk, 0, s>>>(a); break;
+    case P_GATED: gemv_kernel<NCH, MODE, P_GATED><<<grid, blk, 0, s>>>(a); break;
+    case P_LOADQ: gemv_kernel<NCH, MODE, P_LOADQ><<<grid, blk, 0, s>>>(a); break;
+    default: gemv_kernel<NCH, MODE, P_LOAD><<<grid, blk, 0, s>>>(a); break;
+  }
+}
+template <int NCH>
+static void launch_gemv_mode(const GemvArgs& a, int grid, dim3 blk, hipStream_t s) {
+  if (a.mode == M_W8A8)
+    launch_gemv_pro<NCH, M_W8A8>(a, grid, blk, s);
+  else
+    launch_gemv_pro<NCH, M_W8A16>(a, grid, blk, s);
+}
+
+hipError_t launch_gemv(const GemvArgs& a, int waves_per_block, hipStream_t s) {
+  if (a.nseg < 1 || a.nseg > 4 || waves_per_block < 1 || waves_per_block > 4) return hipErrorInvalidValue;
+  if (a.prologue == P_LOADQ && a.mode != M_W8A8) return hipErrorInvalidValue;
+  if (a.prologue == P_GATED && a.K != 2048) return hipErrorInvalidValue;
+  const int total = a.seg[a.nseg - 1].batch0 + a.seg[a.nseg - 1].nbatch;
+  const int grid = (total + waves_per_block - 1) / waves_per_block;
+  const dim3 blk(64 * waves_per_block);
+  switch ((a.K + 1023) / 1024) {
+    case 1: launch_gemv_mode<1>(a, grid, blk, s); break;
+    case 2: launch_gemv_mode<2>(a, grid, blk, s); break;
+    case 3: launch_gemv_mode<3>(a, grid, blk, s); break;
+    case 4: launch_gemv_mode<4>(a, grid, blk, s); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// ===========================================================================
+// Tied LM head: final rmsnorm prologue, logits = (E row . h) * s in C16
+// order, running argmax with the reference's rule (strict >, so the first
+// index wins a tie; qwen_synth.hpp:81-88) folded per block.
+// ===========================================================================
+__device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+__global__ __launch_bounds__(256) void head_kernel(const HeadArgs a) {
+  if (a.done != nullptr && *a.done != 0) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwv = blockDim.x >> 6;
+  float xv[16];
+  load16f(a.h + 16 * lane, xv);
+  float ss = dot16_f32(xv, xv, 0.0f);
+  ss = xor_sum<64>(ss);
+  const float inv = 1.0f / sqrtf(ss / 1024.0f + a.eps);
+  {
+    float w[16];
+    load16f(a.nw + 16 * lane, w);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) xv[e] = (xv[e] * inv) * (1.0f + w[e]);
+  }
+  float bv = -1e30f;
+  int bi = 0;
+  const int total = a.rows / kRowsPerBatch;
+  for (int b = blockIdx.x * nwv + wave; b < total; b += gridDim.x * nwv) {
+    const int row0 = b * kRowsPerBatch;
+    uint32_t w[8][4];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) load16b(a.w + (size_t)(row0 + r) * 1024 + 16 * lane, w[r]);
+    float p[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) p[r] = dot16_i8f(w[r], xv, 0.0f);
+    const float y0 = reduce8(p, lane);
+    const int row = row0 + ((lane >> 3) & 7);
+    const float y = y0 * a.sw[row];
+    if ((lane & 7) == 0) {
+      if (a.logits != nullptr) a.logits[row] = y;
+      better(bv, bi, y, row);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    better(bv, bi, ov, oi);
+  }
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w2 = 1; w2 < nwv; ++w2) better(bv, bi, sv[w2], si[w2]);
+    a.part_val[blockIdx.x] = bv;
+    a.part_idx[blockIdx.x] = bi;
+  }
+}
+
+hipError_t launch_head(const HeadArgs& a, int grid, hipStream_t s) {
+  head_kernel<<<grid, 256, 0, s>>>(a);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(const float* pv, const int* pi, int n, StepCtl* ctl,
+                                                     int* out_idx) {
+  if (ctl != nullptr && ctl->done != 0) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float bv = -1e30f;
+  int bi = 0;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) better(bv, bi, pv[i], pi[i]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    better(bv, bi, ov, oi);
+  }
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w2 = 1; w2 < (int)(blockDim.x >> 6); ++w2) better(bv, bi, sv[w2], si[w2]);
+    if (out_idx != nullptr) *out_idx = bi;
+    if (ctl != nullptr) {
+      ctl->argmax = bi;
+      ctl->pos = ctl->pos + 1;   // qwen_synth.hpp:90 ++st.pos
+    }
+  }
+}
+
+hipError_t launch_argmax(const float* pv, const int* pi, int n, StepCtl* ctl, int* out_idx, hipStream_t s) {
+  argmax_kernel<<<1, 256, 0, s>>>(pv, pi, n, ctl, out_idx);
+  return hipGetLastError();
+}
+
+// Greedy-generation bookkeeping between steps (run_hls.cpp:56-66 on device).
+__global__ void advance_kernel(StepCtl* c, const int* prompt, int* out_ids) {
+  if (c->done != 0) return;
+  const int am = c->argmax;
+  const int next = c->step + 1;
+  if (next < c->n_prompt) {
+    c->tok = prompt[next];
+    c->step = next;
+    return;
+  }
+  if (c->n_out >= c->n_new || am == c->eos) {
+    c->done = 1;
+    return;
+  }
+  out_ids[c->n_out] = am;
+  c->n_out = c->n_out + 1;
+  c->tok = am;
+  c->step = next;
+  if (c->pos >= c->max_ctx) {
+    c->done = 1;
+    c->err = 2;
+  }
+}
+
+hipError_t launch_advance(StepCtl* ctl, const int* prompt, int* out_ids, hipStream_t s) {
+  advance_kernel<<<1, 1, 0, s>>>(ctl, prompt, out_ids);
+  return hipGetLastError();
+}
+
+// ===========================================================================
+// Gated DeltaNet recurrent step (deltanet.hpp:58-127 and the l2norm / q-scale
+// of deltanet.hpp:166-169).  Block (head h, quarter vq) owns S[h][:, 32 vq ..
+// 32 vq + 31] in registers: thread (kg, vl) holds the 16 rows k = 16 kg .. 16
+// kg + 15 of column v = 32 vq + vl.  Sweep A decays S and forms the k-group
+// partial of k^T S; the 8 group partials meet in LDS and are added by the
+// pairwise tree (offsets 4, 2, 1); delta = (v - kv) * beta; sweep B applies
+// the rank-1 update and forms q^T S_new the same way.  S is read and written
+// once per step.
+// ===========================================================================
+__global__ __launch_bounds__(256) void deltanet_kernel(const DnArgs a) {
+  if (a.done != nullptr && *a.done != 0) return;
+  const int h = blockIdx.x / kDnVQuarters, vq = blockIdx.x % kDnVQuarters;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  __shared__ float qs[128], ks[128];
+  __shared__ float part[8][32];
+  __shared__ float dl[32];
+  if (wave < 2) {   // wave 0: q, wave 1: k; lanes 0..7 hold 16 elements each
+    const float* src = a.convd + (wave == 0 ? 0 : 2048) + h * 128;
+    float v[16];
+    float ss = 0.0f;
+    if (lane < 8) {
+      load16f(src + 16 * lane, v);
+      ss = dot16_f32(v, v, 0.0f);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) v[e] = 0.0f;
+    }
+    if (a.normalize) {
+      ss = xor_sum<8>(ss);
+      const float inv = 1.0f / sqrtf(ss + 1e-6f);   // deltanet.hpp:134
+#pragma unroll
+      for (int e = 0; e < 16; ++e) v[e] = v[e] * inv;
+      if (wave == 0) {
+        const float sc = 1.0f / sqrtf(128.0f);   // deltanet.hpp:168-169
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = v[e] * sc;
+      }
+    }
+    if (lane < 8) store16f((wave == 0 ? qs : ks) + 16 * lane, v);
+  }
+  __syncthreads();
+  const int vl = t & 31, kg = t >> 5, v = vq * 32 + vl;
+  const float g = a.gb[h], beta = a.gb[16 + h];
+  const float gexp = dev_expf(g);
+  float* Sh = a.S + (size_t)h * 128 * 128;
+  float s[16];
+  float p = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {   // sweep A
+    const int k = kg * 16 + i;
+    s[i] = Sh[k * 128 + v] * gexp;
+    p = p + s[i] * ks[k];
+  }
+  part[kg][vl] = p;
+  __syncthreads();
+  if (kg == 0) {
+    float pp[8];
+#pragma unroll
+    for (int gi = 0; gi < 8; ++gi) pp[gi] = part[gi][vl];
+#pragma unroll
+    for (int off = 4; off >= 1; off >>= 1)
+#pragma unroll
+      for (int gi = 0; gi < off; ++gi) pp[gi] = pp[gi] + pp[gi + off];
+    const float vv = a.convd[4096 + h * 128 + v];
+    dl[vl] = (vv - pp[0]) * beta;
+  }
+  __syncthreads();
+  const float d = dl[vl];
+  p = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {   // sweep B: reads the updated S
+    const int k = kg * 16 + i;
+    s[i] = s[i] + ks[k] * d;
+    p = p + s[i] * qs[k];
+    Sh[k * 128 + v] = s[i];
+  }
+  part[kg][vl] = p;
+  __syncthreads();
+  if (kg == 0) {
+    float pp[8];
+#pragma unroll
+    for (int gi = 0; gi < 8; ++gi) pp[gi] = part[gi][vl];
+#pragma unroll
+    for (int off = 4; off >= 1; off >>= 1)
+#pragma unroll
+      for (int gi = 0; gi < off; ++gi) pp[gi] = pp[gi] + pp[gi + off];
+    a.o[h * 128 + v] = pp[0];
+  }
+}
+
+hipError_t launch_deltanet(const DnArgs& a, hipStream_t s) {
+  if (a.heads < 1 || a.heads > 16) return hipErrorInvalidValue;
+  deltanet_kernel<<<a.heads * kDnVQuarters, 256, 0, s>>>(a);
+  return hipGetLastError();
+}
+
+// ===========================================================================
+// Gated GQA attention, split-K flash decoding (attention.hpp:25-95).
+// Block (split s, kv head j) covers positions [64 s, 64 s + 64) for the four
+// query heads 4j..4j+3 (GQA kv = h/4).  Each wave normalises and rotates the
+// four queries (QK-norm with (1+w), RoPE on dims 0..63) in the C16 layout:
+// 16 lanes x 16 dims, four positions per wave iteration.  The block owning
+// slot T first writes the new K (normed, rotated) and V rows.  Scores are C16
+// dots scaled by 1/16; per head the split max m, p = exp(s - m), the 64-lane
+// tree sum l and the position-ordered fma sum acc = sum p v are written for
+// the combine step.
+// ===========================================================================
+__device__ __forceinline__ void qk_norm_rope(float* x, const float* nw16, float eps, int g16,
+                                             const float* cs, const float* sn) {
+  float ss = dot16_f32(x, x, 0.0f);
+  ss = xor_sum<16>(ss);
+  const float inv = 1.0f / sqrtf(ss / 256.0f + eps);
+#pragma unroll
+  for (int e = 0; e < 16; ++e) x[e] = (x[e] * inv) * (1.0f + nw16[e]);
+  // rope.hpp:30-41 on dims 0..63 (lanes g16 = 0..3); partner dims +-32 live in lane g16 ^ 2
+  float part[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) part[e] = __shfl_xor(x[e], 2, 64);
+  if (g16 < 4) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int i = 16 * g16 + e;
+      const float half = (i < 32) ? -part[e] : part[e];
+      x[e] = x[e] * cs[i & 31] + half * sn[i & 31];
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
+  if (a.done != nullptr && *a.done != 0) return;
+  const int j = blockIdx.x & 1, s = blockIdx.x >> 1;
+  const int T = *a.T, Tn = T + 1;
+  if (T < 0 || T >= a.max_ctx || s * kAttnSplit >= Tn) return;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int g16 = lane & 15, pg = lane >> 4;
+  const float* cs = a.rope + (size_t)(*a.rope_row) * 64;
+  const float* sn = cs + 32;
+  __shared__ float sc[4][64];
+  __shared__ float pp[4][64];
+  float q[4][16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int h = 4 * j + i;
+    load16f(a.qg + h * 512 + 16 * g16, q[i]);   // query half of head h (attention.hpp:40)
+    float w[16];
+    load16f(a.qn + 16 * g16, w);
+    qk_norm_rope(q[i], w, a.eps, g16, cs, sn);
+  }
+  const int t0 = s * kAttnSplit;
+  if (T / kAttnSplit == s) {   // owner of slot T (attention.hpp:46-54)
+    if (wave == 0) {
+      float k[16], w[16], v[16];
+      load16f(a.kraw + j * 256 + 16 * g16, k);
+      load16f(a.kn + 16 * g16, w);
+      qk_norm_rope(k, w, a.eps, g16, cs, sn);
+      load16f(a.vraw + j * 256 + 16 * g16, v);
+      if (pg == 0) {
+        store16f(a.kc + (size_t)T * 512 + j * 256 + 16 * g16, k);
+        store16f(a.vc + (size_t)T * 512 + j * 256 + 16 * g16, v);
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int tl = 16 * wave + 4 * it + pg;   // position within the split
+    const int tp = t0 + tl;
+    const bool valid = tp < Tn;
+    float k[16];
+    if (valid) {
+      load16f(a.kc + (size_t)tp * 512 + j * 256 + 16 * g16, k);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) k[e] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float d = dot16_f32(q[i], k, 0.0f);
+      d = xor_sum<16>(d);
+      if (g16 == 0) sc[i][tl] = valid ? d * 0.0625f : -__builtin_inff();
+    }
+  }
+  __syncthreads();
+  {
+    const int i = wave;
+    const bool valid = t0 + lane < Tn;
+    const float sv = sc[i][lane];
+    const float m = xor_max<64>(valid ? sv : -__builtin_inff());
+    const float p = valid ? dev_expf(sv - m) : 0.0f;
+    const float l = xor_sum<64>(p);
+    pp[i][lane] = p;
+    if (lane == 0) {
+      a.pm[(4 * j + i) * a.nsplit_max + s] = m;
+      a.pl[(4 * j + i) * a.nsplit_max + s] = l;
+    }
+  }
+  __syncthreads();
+  {
+    const int i = wave;
+    const int cnt = min(kAttnSplit, Tn - t0);
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int tt = 0; tt < cnt; ++tt) {
+      const float pv = pp[i][tt];
+      const float4 vv = *reinterpret_cast<const float4*>(a.vc + (size_t)(t0 + tt) * 512 + j * 256 + 4 * lane);
+      acc[0] = __builtin_fmaf(pv, vv.x, acc[0]);
+      acc[1] = __builtin_fmaf(pv, vv.y, acc[1]);
+      acc[2] = __builtin_fmaf(pv, vv.z, acc[2]);
+      acc[3] = __builtin_fmaf(pv, vv.w, acc[3]);
+    }
+    float4* dst = reinterpret_cast<float4*>(a.pacc + ((size_t)(4 * j + i) * a.nsplit_max + s) * 256 + 4 * lane);
+    *dst = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  }
+}
+
+// Merge the splits of each head in split order; output gate (attention.hpp:89-92).
+__global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
+  if (a.done != nullptr && *a.done != 0) return;
+  const int h = blockIdx.x, d = threadIdx.x;
+  const int T = *a.T, Tn = T + 1;
+  if (T < 0 || T >= a.max_ctx) return;
+  const int ns = (Tn + kAttnSplit - 1) / kAttnSplit;
+  const float* pm = a.pm + h * a.nsplit_max;
+  const float* pl = a.pl + h * a.nsplit_max;
+  float M = -__builtin_inff();
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, pm[s]);
+  float L = 0.0f, ctx = 0.0f;
+  for (int s = 0; s < ns; ++s) {
+    const float e = dev_expf(pm[s] - M);
+    L = L + pl[s] * e;
+    ctx = ctx + a.pacc[((size_t)h * a.nsplit_max + s) * 256 + d] * e;
+  }
+  const float invL = 1.0f / L;
+  const float gate = a.qg[h * 512 + 256 + d];
+  a.og[h * 256 + d] = (ctx * invL) * dev_sigmoid(gate);
+}
+
+hipError_t launch_attn(const AttnArgs& a, hipStream_t s) {
+  attn_kernel<<<2 * a.nsplit_max, 256, 0, s>>>(a);
+  return hipGetLastError();
+}
+hipError_t launch_attn_combine(const AttnArgs& a, hipStream_t s) {
+  attn_combine_kernel<<<8, 256, 0, s>>>(a);
+  return hipGetLastError();
+}
+
+// ===========================================================================
+// Small op-level kernels.
+// ===========================================================================
+__global__ void embed_kernel(float* h, const int8_t* w, const float* sc, int tok, int in) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < in) h[i] = (float)w[(size_t)tok * in + i] * sc[tok];
+}
+hipError_t launch_embed(float* h, const int8_t* w, const float* sc, int tok, int in, hipStream_t s) {
+  embed_kernel<<<(in + 255) / 256, 256, 0, s>>>(h, w, sc, tok, in);
+  return hipGetLastError();
+}
+
+// one wave: C16 sum of squares over n, then the (1+w) or gated scaling.
+__global__ void rmsnorm_kernel(float* y, const float* x, const float* w, const float* z, int n, float eps,
+                               int gated) {
+  const int lane = threadIdx.x;
+  const int nchunk = (n + 15) / 16;
+  float ss = 0.0f;
+  for (int c = lane; c < nchunk; c += 64)
+    for (int e = 0; e < 16 && 16 * c + e < n; ++e) ss = __builtin_fmaf(x[16 * c + e], x[16 * c + e], ss);
+  ss = xor_sum<64>(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+  for (int c = lane; c < nchunk; c += 64)
+    for (int e = 0; e < 16 && 16 * c + e < n; ++e) {
+      const int i = 16 * c + e;
+      y[i] = gated ? ((x[i] * inv) * w[i]) * dev_silu(z[i]) : (x[i] * inv) * (1.0f + w[i]);
+    }
+}
+hipError_t launch_rmsnorm(float* y, const float* x, const float* w, const float* z, int n, float eps,
+                          int gated, hipStream_t s) {
+  rmsnorm_kernel<<<1, 64, 0, s>>>(y, x, w, z, n, eps, gated);
+  return hipGetLastError();
+}
+
+__global__ void l2norm_kernel(float* v, int n) {
+  const int lane = threadIdx.x;
+  const int nchunk = (n + 15) / 16;
+  float ss = 0.0f;
+  for (int c = lane; c < nchunk; c += 64)
+    for (int e = 0; e < 16 && 16 * c + e < n; ++e) ss = __builtin_fmaf(v[16 * c + e], v[16 * c + e], ss);
+  ss = xor_sum<64>(ss);
+  const float inv = 1.0f / sqrtf(ss + 1e-6f);
+  for (int c = lane; c < nchunk; c += 64)
+    for (int e = 0; e < 16 && 16 * c + e < n; ++e) v[16 * c + e] = v[16 * c + e] * inv;
+}
+hipError_t launch_l2norm(float* v, int n, hipStream_t s) {
+  l2norm_kernel<<<1, 64, 0, s>>>(v, n);
+  return hipGetLastError();
+}
+
+__global__ void conv1d_kernel(float* out, const float* in, float* state, const float* w, int C) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  float* st = state + (size_t)c * 4;
+  const float* wc = w + (size_t)c * 4;
+  const float w0 = st[1], w1 = st[2], w2 = st[3], w3 = in[c];
+  float acc = 0.0f;
+  acc = acc + w0 * wc[0];
+  acc = acc + w1 * wc[1];
+  acc = acc + w2 * wc[2];
+  acc = acc + w3 * wc[3];
+  st[0] = w0;
+  st[1] = w1;
+  st[2] = w2;
+  st[3] = w3;
+  out[c] = dev_silu(acc);
+}
+hipError_t launch_conv1d(float* out, const float* in, float* state, const float* w, int C, hipStream_t s) {
+  conv1d_kernel<<<(C + 255) / 256, 256, 0, s>>>(out, in, state, w, C);
+  return hipGetLastError();
+}
+
+__global__ void apply_rope_kernel(float* x, const float* cs, const float* sn) {
+  const int i = threadIdx.x;   // 64 lanes: dims 0..63
+  const float r = x[i];
+  const float partner = __shfl_xor(r, 32, 64);
+  const float half = (i < 32) ? -partner : partner;
+  x[i] = r * cs[i] + half * sn[i];
+}
+hipError_t launch_apply_rope(float* x, const float* cs, const float* sn, hipStream_t s) {
+  apply_rope_kernel<<<1, 64, 0, s>>>(x, cs, sn);
+  return hipGetLastError();
+}
+
+__global__ void quant_kernel(int8_t* q, float* sx, const float* x, int n) {
+  __shared__ float sm[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float am = 0.0f;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) am = fmaxf(am, fabsf(x[i]));
+  am = xor_max<64>(am);
+  if (lane == 0) sm[wave] = am;
+  __syncthreads();
+  am = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
+  const float s = quant_scale(am);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) q[i] = (int8_t)quant_one(x[i], s);
+  if (threadIdx.x == 0) *sx = s;
+}
+hipError_t launch_quant(int8_t* q, float* sx, const float* x, int n, hipStream_t s) {
+  quant_kernel<<<1, 256, 0, s>>>(q, sx, x, n);
+  return hipGetLastError();
+}
+
+__global__ void set_ints_kernel(int* dst, int a, int b) {
+  dst[0] = a;
+  dst[1] = b;
+}
+hipError_t launch_set_ints(int* dst, int a, int b, hipStream_t s) {
+  set_ints_kernel<<<1, 1, 0, s>>>(dst, a, b);
+  return hipGetLastError();
+}
+
+__global__ void set_int_kernel(int* dst, int v) { *dst = v; }
+hipError_t launch_set_int(int* dst, int v, hipStream_t s) {
+  set_int_kernel<<<1, 1, 0, s>>>(dst, v);
+  return hipGetLastError();
+}
+
+__global__ void set_floats_kernel(float* dst, const Floats64 v, int n) {
+  if ((int)threadIdx.x < n) dst[threadIdx.x] = v.v[threadIdx.x];
+}
+hipError_t launch_set_floats(float* dst, const Floats64& v, int n, hipStream_t s) {
+  if (n < 0 || n > 64) return hipErrorInvalidValue;
+  set_floats_kernel<<<1, 64, 0, s>>>(dst, v, n);
+  return hipGetLastError();
+}
+
+// pos += 1 for a layer-range step (no head / argmax); honours the stop flag.
+__global__ void bump_pos_kernel(StepCtl* c) {
+  if (c->done == 0) c->pos = c->pos + 1;
+}
+hipError_t launch_bump_pos(StepCtl* ctl, hipStream_t s) {
+  bump_pos_kernel<<<1, 1, 0, s>>>(ctl);
+  return hipGetLastError();
+}
+
+__global__ void init_gen_kernel(StepCtl* c, int tok0, int n_prompt, int n_new, int eos) {
+  c->tok = tok0;
+  c->step = 0;
+  c->n_prompt = n_prompt;
+  c->n_new = n_new;
+  c->n_out = 0;
+  c->eos = eos;
+  c->done = 0;
+  c->err = 0;
+}
+hipError_t launch_init_gen(StepCtl* ctl, int tok0, int n_prompt, int n_new, int eos, hipStream_t s) {
+  init_gen_kernel<<<1, 1, 0, s>>>(ctl, tok0, n_prompt, n_new, eos);
+  return hipGetLastError();
+}
+
+__global__ void store_gb_kernel(float* gb, float g, float beta) {
+  gb[0] = g;
+  gb[16] = beta;
+}
+hipError_t launch_store_gb(float* gb, float g, float beta, hipStream_t s) {
+  store_gb_kernel<<<1, 1, 0, s>>>(gb, g, beta);
+  return hipGetLastError();
+}
+
+}  // namespace qh

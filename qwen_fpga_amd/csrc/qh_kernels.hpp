@@ -1,0 +1,152 @@
+// Kernel argument structs and launch wrappers shared by the op-level C ABI
+// (qh_ops.hip) and the engine (qh_engine.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qh {
+
+constexpr int kRowsPerBatch = 8;     // rows one wave reduces together
+constexpr int kAttnSplit = 64;       // positions per attention split
+constexpr int kDnVQuarters = 4;      // DeltaNet workgroups per head (32 v columns each)
+
+enum SegKind : int { SEG_I8 = 0, SEG_F32 = 1, SEG_PAIR = 2 };
+enum Epi : int {
+  E_STORE = 0,   // out[row] = y
+  E_RESID = 1,   // out[row] = out[row] + y                    (h = r + mix)
+  E_CONV = 2,    // depthwise conv + SiLU into out, state c2 updated (conv1d.hpp:17-38)
+  E_GATE_B = 3,  // out[row] = sigmoid(y)                     (beta, deltanet.hpp:164)
+  E_GATE_A = 4,  // out[row] = -exp(A_log)*softplus(y+dt_bias) (g, deltanet.hpp:165)
+  E_SWIGLU = 5,  // pair rows (gate i, up i): out[i] = silu(g)*u (mlp.hpp:17)
+  E_ACC = 6,     // out[row] = y and acc_out[row] = int32 accumulator (W8A8 op)
+};
+enum Prologue : int {
+  P_LOAD = 0,    // x[K] fp32 as given
+  P_NORM = 1,    // rmsnorm(x, nw) with (1+w) (norm.hpp:13-20); optional embed row first
+  P_GATED = 2,   // per-head rmsnorm_gated(o, nw, z) over 16 x 128 (deltanet.hpp:177-179)
+  P_LOADQ = 3,   // int8 xq[K] + scale sx given (W8A8 op)
+};
+enum Mode : int { M_W8A16 = 0, M_W8A8 = 1 };
+
+struct Seg {
+  int kind = SEG_I8, epi = E_STORE;
+  int batch0 = 0, nbatch = 0, rows = 0;   // batch range in the launch; valid rows
+  const int8_t* w = nullptr;              // int8 [rows][K]
+  const float* sw = nullptr;              // fp32 [rows] per-row scales
+  const float* wf = nullptr;              // fp32 [rows][K] (SEG_F32)
+  const int8_t* w2 = nullptr;             // SEG_PAIR second matrix (up)
+  const float* sw2 = nullptr;
+  float* out = nullptr;
+  int32_t* acc_out = nullptr;
+  const float* c0 = nullptr;              // E_CONV: taps [C][4]   E_GATE_A: A_log
+  const float* c1 = nullptr;              // E_GATE_A: dt_bias
+  float* c2 = nullptr;                    // E_CONV: state [C][4]
+};
+
+struct GemvArgs {
+  int K = 0, mode = M_W8A16, prologue = P_LOAD;
+  const float* x = nullptr;     // P_LOAD / P_NORM input, P_GATED o
+  const float* nw = nullptr;    // P_NORM [K] gain, P_GATED [128] gain
+  const float* z = nullptr;     // P_GATED gate input [2048]
+  const int8_t* xq = nullptr;   // P_LOADQ
+  const float* sx = nullptr;
+  float eps = 1e-6f;
+  const int8_t* emb = nullptr;  // P_NORM: if set, x = emb[tok]*emb_s[tok] (gemv.hpp:76-84)
+  const float* emb_s = nullptr;
+  const int* tok = nullptr;
+  float* h_out = nullptr;       // receives the embedded row (block 0)
+  const int* done = nullptr;    // engine stop flag (skip when *done != 0)
+  int nseg = 0;
+  Seg seg[4];
+};
+
+// LM head (tied embedding): logits = (E h_norm) * s, running argmax per block.
+struct HeadArgs {
+  const float* h = nullptr;     // [1024] final hidden (pre-norm)
+  const float* nw = nullptr;    // final norm gain
+  float eps = 1e-6f;
+  const int8_t* w = nullptr;    // [rows][1024]
+  const float* sw = nullptr;
+  int rows = 0;
+  float* logits = nullptr;      // optional [rows]
+  float* part_val = nullptr;    // [grid] block maxima
+  int* part_idx = nullptr;
+  const int* done = nullptr;
+};
+
+// Decode-step control block, device resident.
+struct StepCtl {
+  int tok;        // token fed this step
+  int pos;        // tokens already processed (RoPE position and KV slot)
+  int argmax;     // result of the last step
+  int step;       // index of the fed token in prompt order (generation driver)
+  int n_prompt;
+  int n_new;
+  int n_out;
+  int eos;
+  int done;
+  int err;        // 1: token id out of range; 2: context full
+  int max_ctx;
+  int pad;
+};
+
+struct AttnArgs {
+  const float* qg = nullptr;     // [4096] q || gate interleaved per head
+  const float* kraw = nullptr;   // [512]
+  const float* vraw = nullptr;   // [512]
+  const float* qn = nullptr;     // q_norm [256]
+  const float* kn = nullptr;     // k_norm [256]
+  const float* rope = nullptr;   // [rows][64]: cos[32] then sin[32] per row
+  float* kc = nullptr;           // [max_ctx][512]
+  float* vc = nullptr;
+  const int* T = nullptr;        // slot of this token (past tokens = T)
+  const int* rope_row = nullptr; // row of `rope` to use
+  float* pm = nullptr;           // [8][nsplit] split maxima
+  float* pl = nullptr;           // [8][nsplit] split sums
+  float* pacc = nullptr;         // [8][nsplit][256]
+  int nsplit_max = 0;
+  int max_ctx = 0;               // rows of kc / vc; a slot T >= max_ctx is never touched
+  float* og = nullptr;           // combine output [2048]
+  float eps = 1e-6f;
+  const int* done = nullptr;
+};
+
+struct DnArgs {
+  const float* convd = nullptr;  // [6144] post-conv q | k | v
+  const float* gb = nullptr;     // g[16] then beta[16]
+  float* S = nullptr;            // [16][128][128]
+  float* o = nullptr;            // [16][128]
+  int normalize = 1;             // l2norm q,k and scale q (0: given already normalized)
+  int heads = 16;                // heads to process (1 for the single-head op)
+  const int* done = nullptr;
+};
+
+struct Floats64 { float v[64]; };
+
+// ---- launch wrappers (return hipError_t) ----
+hipError_t launch_gemv(const GemvArgs& a, int waves_per_block, hipStream_t s);
+hipError_t launch_head(const HeadArgs& a, int grid, hipStream_t s);
+hipError_t launch_argmax(const float* pv, const int* pi, int n, StepCtl* ctl, int* out_idx,
+                         hipStream_t s);
+hipError_t launch_deltanet(const DnArgs& a, hipStream_t s);
+hipError_t launch_attn(const AttnArgs& a, hipStream_t s);
+hipError_t launch_attn_combine(const AttnArgs& a, hipStream_t s);
+hipError_t launch_advance(StepCtl* ctl, const int* prompt, int* out_ids, hipStream_t s);
+
+// small op kernels
+hipError_t launch_embed(float* h, const int8_t* w, const float* sc, int tok, int in, hipStream_t s);
+hipError_t launch_rmsnorm(float* y, const float* x, const float* w, const float* z, int n, float eps,
+                          int gated, hipStream_t s);
+hipError_t launch_l2norm(float* v, int n, hipStream_t s);
+hipError_t launch_conv1d(float* out, const float* in, float* state, const float* w, int C,
+                         hipStream_t s);
+hipError_t launch_apply_rope(float* x, const float* cs, const float* sn, hipStream_t s);
+hipError_t launch_quant(int8_t* q, float* sx, const float* x, int n, hipStream_t s);
+hipError_t launch_set_ints(int* dst, int a, int b, hipStream_t s);
+hipError_t launch_set_int(int* dst, int v, hipStream_t s);
+hipError_t launch_store_gb(float* gb, float g, float beta, hipStream_t s);
+hipError_t launch_set_floats(float* dst, const Floats64& v, int n, hipStream_t s);
+hipError_t launch_bump_pos(StepCtl* ctl, hipStream_t s);
+hipError_t launch_init_gen(StepCtl* ctl, int tok0, int n_prompt, int n_new, int eos, hipStream_t s);
+
+}  // namespace qh

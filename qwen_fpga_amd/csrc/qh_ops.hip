@@ -1,0 +1,506 @@
+// Op-level C ABI: the reference's per-kernel contracts (hls/src/*.hpp) on the
+// device.  Every function validates its arguments on the host, enqueues on the
+// caller's stream and returns without synchronising.  Layer ops that need
+// intermediate buffers take them from the stream-ordered allocator
+// (hipMallocAsync / hipFreeAsync on the same stream), so they stay reentrant.
+#include <cmath>
+#include <cstring>
+
+#include "qh_common.hpp"
+#include "qh_kernels.hpp"
+#include "qh_layout.hpp"
+
+using namespace qh;
+
+namespace qh {
+
+void rope_row(int pos, float* out64) {
+  for (int j = 0; j < kRopeDim / 2; ++j) {
+    const float inv = 1.0f / std::pow(kRopeTheta, float(2 * j) / float(kRopeDim));
+    const float f = (float)pos * inv;
+    out64[j] = std::cos(f);
+    out64[32 + j] = std::sin(f);
+  }
+}
+
+}  // namespace qh
+
+namespace {
+
+hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Stream-ordered scratch: one allocation carved into 256-byte aligned pieces.
+struct Scratch {
+  hipStream_t s;
+  char* base = nullptr;
+  size_t size = 0, used = 0;
+  explicit Scratch(hipStream_t st) : s(st) {}
+  int alloc(size_t total) {
+    size = total;
+    return hip_status(hipMallocAsync(reinterpret_cast<void**>(&base), total, s));
+  }
+  template <class T>
+  T* take(size_t n) {
+    const size_t bytes = (n * sizeof(T) + 255) & ~(size_t)255;
+    T* p = reinterpret_cast<T*>(base + used);
+    used += bytes;
+    return p;
+  }
+  ~Scratch() {
+    if (base) (void)hipFreeAsync(base, s);
+  }
+};
+size_t rnd(size_t bytes) { return (bytes + 255) & ~(size_t)255; }
+
+bool tensor_i8(const qh_tensor* t, int out, int in) {
+  return t && t->w_i8 && t->scale && t->out == out && t->in == in && aligned16(t->w_i8);
+}
+bool tensor_f32(const qh_tensor* t, int out, int in) {
+  return t && t->w_f32 && t->out == out && t->in == in && aligned16(t->w_f32);
+}
+
+Seg seg_i8(const int8_t* w, const float* sw, int rows, int batch0, float* out, int epi) {
+  Seg g;
+  g.kind = SEG_I8;
+  g.epi = epi;
+  g.batch0 = batch0;
+  g.rows = rows;
+  g.nbatch = (rows + kRowsPerBatch - 1) / kRowsPerBatch;
+  g.w = w;
+  g.sw = sw;
+  g.out = out;
+  return g;
+}
+
+int check_gemv_shape(int out, int in) {
+  if (out <= 0 || in <= 0 || in % 16 != 0 || in > 4096) return QH_EINVAL;
+  return QH_OK;
+}
+
+// ---- layer compositions (shared by the W8A16 and W8A8 entry points) ----
+int deltanet_layer(float* out, const float* x, const qh_tensor* qkv_w, const qh_tensor* z_w,
+                   const qh_tensor* b_w, const qh_tensor* a_w, const float* conv_w, const float* A_log,
+                   const float* dt_bias, const float* gate_norm_w, const qh_tensor* out_w, float* rec,
+                   float* conv_state, int mode, hipStream_t s) {
+  if (!out || !x || !conv_w || !A_log || !dt_bias || !gate_norm_w || !rec || !conv_state) return QH_EINVAL;
+  if (!tensor_i8(qkv_w, kConvDim, kHidden) || !tensor_i8(z_w, kZDim, kHidden) ||
+      !tensor_f32(b_w, kLH, kHidden) || !tensor_f32(a_w, kLH, kHidden) ||
+      !tensor_i8(out_w, kHidden, kLH * kLV))
+    return QH_EINVAL;
+  if (!aligned16(x) || !aligned16(gate_norm_w)) return QH_EINVAL;
+  Scratch sc(s);
+  QH_TRY(sc.alloc(rnd(4 * kConvDim) + rnd(4 * kZDim) + rnd(4 * 32) + rnd(4 * kLH * kLV)));
+  float* convd = sc.take<float>(kConvDim);
+  float* zb = sc.take<float>(kZDim);
+  float* gb = sc.take<float>(32);
+  float* o = sc.take<float>(kLH * kLV);
+  // in_proj_qkv / z / b / a over the shared activation (deltanet.hpp:149-152, model.py:143-147)
+  GemvArgs a;
+  a.K = kHidden;
+  a.mode = mode;
+  a.prologue = P_LOAD;
+  a.x = x;
+  a.nseg = 4;
+  int b0 = 0;
+  a.seg[0] = seg_i8(qkv_w->w_i8, qkv_w->scale, kConvDim, b0, convd, E_CONV);
+  a.seg[0].c0 = conv_w;
+  a.seg[0].c2 = conv_state;
+  b0 += a.seg[0].nbatch;
+  a.seg[1] = seg_i8(z_w->w_i8, z_w->scale, kZDim, b0, zb, E_STORE);
+  b0 += a.seg[1].nbatch;
+  Seg gbeta;
+  gbeta.kind = SEG_F32;
+  gbeta.epi = E_GATE_B;
+  gbeta.batch0 = b0;
+  gbeta.rows = kLH;
+  gbeta.nbatch = kLH / kRowsPerBatch;
+  gbeta.wf = b_w->w_f32;
+  gbeta.out = gb + 16;
+  a.seg[2] = gbeta;
+  b0 += gbeta.nbatch;
+  Seg ga = gbeta;
+  ga.epi = E_GATE_A;
+  ga.batch0 = b0;
+  ga.wf = a_w->w_f32;
+  ga.out = gb;
+  ga.c0 = A_log;
+  ga.c1 = dt_bias;
+  a.seg[3] = ga;
+  QH_HIP(launch_gemv(a, 4, s));
+  DnArgs d;
+  d.convd = convd;
+  d.gb = gb;
+  d.S = rec;
+  d.o = o;
+  QH_HIP(launch_deltanet(d, s));
+  GemvArgs c;   // gated norm -> out_proj (deltanet.hpp:177-181, model.py:191)
+  c.K = kLH * kLV;
+  c.mode = mode;
+  c.prologue = P_GATED;
+  c.x = o;
+  c.nw = gate_norm_w;
+  c.z = zb;
+  c.nseg = 1;
+  c.seg[0] = seg_i8(out_w->w_i8, out_w->scale, kHidden, 0, out, E_STORE);
+  QH_HIP(launch_gemv(c, 1, s));
+  return QH_OK;
+}
+
+int attention_layer(float* out, const float* x, const qh_tensor* q_w, const qh_tensor* k_w,
+                    const qh_tensor* v_w, const qh_tensor* o_w, const float* q_norm, const float* k_norm,
+                    int pos, float* kcache, float* vcache, int T, int mode, hipStream_t s) {
+  if (!out || !x || !q_norm || !k_norm || !kcache || !vcache) return QH_EINVAL;
+  if (T < 0 || pos < 0) return QH_ERANGE;
+  if (!tensor_i8(q_w, kQProj, kHidden) || !tensor_i8(k_w, kKVProj, kHidden) ||
+      !tensor_i8(v_w, kKVProj, kHidden) || !tensor_i8(o_w, kHidden, kNH * kHD))
+    return QH_EINVAL;
+  if (!aligned16(x) || !aligned16(q_norm) || !aligned16(k_norm) || !aligned16(kcache) || !aligned16(vcache))
+    return QH_EINVAL;
+  const int Tn = T + 1;
+  const int ns = (Tn + kAttnSplit - 1) / kAttnSplit;
+  Scratch sc(s);
+  QH_TRY(sc.alloc(rnd(4 * kQProj) + 2 * rnd(4 * kKVProj) + rnd(4 * 64) + rnd(8) + 2 * rnd(4 * 8 * (size_t)ns) +
+                  rnd(4 * 8 * 256 * (size_t)ns) + rnd(4 * kNH * kHD)));
+  float* qg = sc.take<float>(kQProj);
+  float* kraw = sc.take<float>(kKVProj);
+  float* vraw = sc.take<float>(kKVProj);
+  float* rope = sc.take<float>(64);
+  int* ints = sc.take<int>(2);
+  float* pm = sc.take<float>(8 * (size_t)ns);
+  float* pl = sc.take<float>(8 * (size_t)ns);
+  float* pacc = sc.take<float>(8 * 256 * (size_t)ns);
+  float* og = sc.take<float>(kNH * kHD);
+  GemvArgs a;   // q / k / v projections (attention.hpp:31-33, model.py:200-207)
+  a.K = kHidden;
+  a.mode = mode;
+  a.prologue = P_LOAD;
+  a.x = x;
+  a.nseg = 3;
+  a.seg[0] = seg_i8(q_w->w_i8, q_w->scale, kQProj, 0, qg, E_STORE);
+  a.seg[1] = seg_i8(k_w->w_i8, k_w->scale, kKVProj, a.seg[0].nbatch, kraw, E_STORE);
+  a.seg[2] = seg_i8(v_w->w_i8, v_w->scale, kKVProj, a.seg[0].nbatch + a.seg[1].nbatch, vraw, E_STORE);
+  QH_HIP(launch_gemv(a, 4, s));
+  Floats64 r;
+  rope_row(pos, r.v);
+  QH_HIP(launch_set_floats(rope, r, 64, s));
+  QH_HIP(launch_set_ints(ints, T, 0, s));
+  AttnArgs at;
+  at.qg = qg;
+  at.kraw = kraw;
+  at.vraw = vraw;
+  at.qn = q_norm;
+  at.kn = k_norm;
+  at.rope = rope;
+  at.kc = kcache;
+  at.vc = vcache;
+  at.T = ints;
+  at.rope_row = ints + 1;
+  at.pm = pm;
+  at.pl = pl;
+  at.pacc = pacc;
+  at.nsplit_max = ns;
+  at.max_ctx = Tn;
+  at.og = og;
+  QH_HIP(launch_attn(at, s));
+  QH_HIP(launch_attn_combine(at, s));
+  GemvArgs c;   // o_proj (attention.hpp:94, model.py:230)
+  c.K = kNH * kHD;
+  c.mode = mode;
+  c.prologue = P_LOAD;
+  c.x = og;
+  c.nseg = 1;
+  c.seg[0] = seg_i8(o_w->w_i8, o_w->scale, kHidden, 0, out, E_STORE);
+  QH_HIP(launch_gemv(c, 1, s));
+  return QH_OK;
+}
+
+int mlp_layer(float* out, const float* x, const qh_tensor* gate_w, const qh_tensor* up_w,
+              const qh_tensor* down_w, int mode, hipStream_t s) {
+  if (!out || !x || !aligned16(x)) return QH_EINVAL;
+  if (!tensor_i8(gate_w, kInter, kHidden) || !tensor_i8(up_w, kInter, kHidden) ||
+      !tensor_i8(down_w, kHidden, kInter))
+    return QH_EINVAL;
+  Scratch sc(s);
+  QH_TRY(sc.alloc(rnd(4 * kInter)));
+  float* act = sc.take<float>(kInter);
+  GemvArgs a;   // gate || up as row pairs, SwiGLU in the epilogue (mlp.hpp:14-17)
+  a.K = kHidden;
+  a.mode = mode;
+  a.prologue = P_LOAD;
+  a.x = x;
+  a.nseg = 1;
+  Seg g;
+  g.kind = SEG_PAIR;
+  g.epi = E_SWIGLU;
+  g.rows = 2 * kInter;
+  g.nbatch = 2 * kInter / kRowsPerBatch;
+  g.w = gate_w->w_i8;
+  g.sw = gate_w->scale;
+  g.w2 = up_w->w_i8;
+  g.sw2 = up_w->scale;
+  g.out = act;
+  a.seg[0] = g;
+  QH_HIP(launch_gemv(a, 4, s));
+  GemvArgs c;   // down (mlp.hpp:18, model.py:237)
+  c.K = kInter;
+  c.mode = mode;
+  c.prologue = P_LOAD;
+  c.x = act;
+  c.nseg = 1;
+  c.seg[0] = seg_i8(down_w->w_i8, down_w->scale, kHidden, 0, out, E_STORE);
+  QH_HIP(launch_gemv(c, 1, s));
+  return QH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* qh_strerror(int st) {
+  switch (st) {
+    case QH_OK: return "ok";
+    case QH_EINVAL: return "invalid argument";
+    case QH_ERANGE: return "token id, position or context out of range";
+    case QH_EIO: return "file open/read/map failed";
+    case QH_EFORMAT: return "weight index or blob does not match the packed layout";
+    case QH_ENOMEM: return "allocation failed";
+    case QH_ESTATE: return "engine state does not allow the call";
+    default: return st > 0 ? hipGetErrorString((hipError_t)st) : "unknown status";
+  }
+}
+
+int qh_gemv_i8(float* y, const int8_t* w, const float* scale, const float* x, int out, int in, void* stream) {
+  if (!y || !w || !scale || !x || !aligned16(w) || !aligned16(x)) return QH_EINVAL;
+  QH_TRY(check_gemv_shape(out, in));
+  GemvArgs a;
+  a.K = in;
+  a.mode = M_W8A16;
+  a.prologue = P_LOAD;
+  a.x = x;
+  a.nseg = 1;
+  a.seg[0] = seg_i8(w, scale, out, 0, y, E_STORE);
+  return hip_status(launch_gemv(a, 4, S(stream)));
+}
+
+int qh_gemv_f32(float* y, const float* w, const float* x, int out, int in, void* stream) {
+  if (!y || !w || !x || !aligned16(w) || !aligned16(x)) return QH_EINVAL;
+  QH_TRY(check_gemv_shape(out, in));
+  GemvArgs a;
+  a.K = in;
+  a.mode = M_W8A16;
+  a.prologue = P_LOAD;
+  a.x = x;
+  a.nseg = 1;
+  Seg g;
+  g.kind = SEG_F32;
+  g.epi = E_STORE;
+  g.rows = out;
+  g.nbatch = (out + kRowsPerBatch - 1) / kRowsPerBatch;
+  g.wf = w;
+  g.out = y;
+  a.seg[0] = g;
+  return hip_status(launch_gemv(a, 4, S(stream)));
+}
+
+int qh_row_dot_i8(float* result, const int8_t* w, const float* scale, const float* h, int row, int in,
+                  void* stream) {
+  if (!result || !w || !scale || !h || row < 0) return QH_EINVAL;
+  const int8_t* r = w + (size_t)row * in;
+  if (!aligned16(r) || !aligned16(h)) return QH_EINVAL;
+  QH_TRY(check_gemv_shape(1, in));
+  GemvArgs a;
+  a.K = in;
+  a.mode = M_W8A16;
+  a.prologue = P_LOAD;
+  a.x = h;
+  a.nseg = 1;
+  a.seg[0] = seg_i8(r, scale + row, 1, 0, result, E_STORE);
+  return hip_status(launch_gemv(a, 1, S(stream)));
+}
+
+int qh_embed_row(float* h, const int8_t* w, const float* scale, int tok, int in, void* stream) {
+  if (!h || !w || !scale || in <= 0) return QH_EINVAL;
+  if (tok < 0) return QH_ERANGE;
+  return hip_status(launch_embed(h, w, scale, tok, in, S(stream)));
+}
+
+int qh_rmsnorm(float* y, const float* x, const float* w, int n, float eps, void* stream) {
+  if (!y || !x || !w || n <= 0) return QH_EINVAL;
+  return hip_status(launch_rmsnorm(y, x, w, nullptr, n, eps, 0, S(stream)));
+}
+
+int qh_rmsnorm_gated(float* y, const float* x, const float* w, const float* z, int n, float eps,
+                     void* stream) {
+  if (!y || !x || !w || !z || n <= 0) return QH_EINVAL;
+  return hip_status(launch_rmsnorm(y, x, w, z, n, eps, 1, S(stream)));
+}
+
+int qh_conv1d_step(float* out, const float* in_ch, float* state, const float* weight, void* stream) {
+  if (!out || !in_ch || !state || !weight) return QH_EINVAL;
+  return hip_status(launch_conv1d(out, in_ch, state, weight, kConvDim, S(stream)));
+}
+
+int qh_rope_cos_sin(int pos, float* cos_o, float* sin_o, void* stream) {
+  if (!cos_o || !sin_o) return QH_EINVAL;
+  if (pos < 0) return QH_ERANGE;
+  float r[64];
+  rope_row(pos, r);
+  Floats64 c, sn;   // rope.hpp:24-25: halves mirrored
+  for (int j = 0; j < 32; ++j) {
+    c.v[j] = c.v[j + 32] = r[j];
+    sn.v[j] = sn.v[j + 32] = r[32 + j];
+  }
+  QH_HIP(launch_set_floats(cos_o, c, 64, S(stream)));
+  return hip_status(launch_set_floats(sin_o, sn, 64, S(stream)));
+}
+
+int qh_apply_rope(float* x, const float* cos_, const float* sin_, void* stream) {
+  if (!x || !cos_ || !sin_) return QH_EINVAL;
+  return hip_status(launch_apply_rope(x, cos_, sin_, S(stream)));
+}
+
+int qh_l2norm(float* v, int n, void* stream) {
+  if (!v || n <= 0) return QH_EINVAL;
+  return hip_status(launch_l2norm(v, n, S(stream)));
+}
+
+int qh_delta_rule_head(const float* q, const float* k, const float* v, float g, float beta, float* S_,
+                       float* out, void* stream) {
+  if (!q || !k || !v || !S_ || !out) return QH_EINVAL;
+  hipStream_t s = S(stream);
+  Scratch sc(s);
+  QH_TRY(sc.alloc(rnd(4 * kConvDim) + rnd(4 * 32)));
+  float* convd = sc.take<float>(kConvDim);
+  float* gb = sc.take<float>(32);
+  QH_HIP(hipMemcpyAsync(convd, q, 4 * kLK, hipMemcpyDeviceToDevice, s));
+  QH_HIP(hipMemcpyAsync(convd + 2048, k, 4 * kLK, hipMemcpyDeviceToDevice, s));
+  QH_HIP(hipMemcpyAsync(convd + 4096, v, 4 * kLV, hipMemcpyDeviceToDevice, s));
+  QH_HIP(launch_store_gb(gb, g, beta, s));
+  DnArgs d;
+  d.convd = convd;
+  d.gb = gb;
+  d.S = S_;
+  d.o = out;
+  d.normalize = 0;
+  d.heads = 1;
+  return hip_status(launch_deltanet(d, s));
+}
+
+int qh_delta_rule_layer(const float* q, const float* k, const float* v, const float* g, const float* beta,
+                        float* S_, float* out, void* stream) {
+  if (!q || !k || !v || !g || !beta || !S_ || !out) return QH_EINVAL;
+  hipStream_t s = S(stream);
+  Scratch sc(s);
+  QH_TRY(sc.alloc(rnd(4 * kConvDim) + rnd(4 * 32)));
+  float* convd = sc.take<float>(kConvDim);
+  float* gb = sc.take<float>(32);
+  QH_HIP(hipMemcpyAsync(convd, q, 4 * 2048, hipMemcpyDeviceToDevice, s));
+  QH_HIP(hipMemcpyAsync(convd + 2048, k, 4 * 2048, hipMemcpyDeviceToDevice, s));
+  QH_HIP(hipMemcpyAsync(convd + 4096, v, 4 * 2048, hipMemcpyDeviceToDevice, s));
+  QH_HIP(hipMemcpyAsync(gb, g, 4 * 16, hipMemcpyDeviceToDevice, s));
+  QH_HIP(hipMemcpyAsync(gb + 16, beta, 4 * 16, hipMemcpyDeviceToDevice, s));
+  DnArgs d;
+  d.convd = convd;
+  d.gb = gb;
+  d.S = S_;
+  d.o = out;
+  d.normalize = 0;
+  d.heads = 16;
+  return hip_status(launch_deltanet(d, s));
+}
+
+int qh_deltanet_layer(float* out, const float* x, const qh_tensor* qkv_w, const qh_tensor* z_w,
+                      const qh_tensor* b_w, const qh_tensor* a_w, const float* conv_w, const float* A_log,
+                      const float* dt_bias, const float* gate_norm_w, const qh_tensor* out_w, float* rec,
+                      float* conv_state, void* stream) {
+  return deltanet_layer(out, x, qkv_w, z_w, b_w, a_w, conv_w, A_log, dt_bias, gate_norm_w, out_w, rec,
+                        conv_state, M_W8A16, S(stream));
+}
+int qh_deltanet_layer_w8a8(float* out, const float* x, const qh_tensor* qkv_w, const qh_tensor* z_w,
+                           const qh_tensor* b_w, const qh_tensor* a_w, const float* conv_w,
+                           const float* A_log, const float* dt_bias, const float* gate_norm_w,
+                           const qh_tensor* out_w, float* rec, float* conv_state, void* stream) {
+  return deltanet_layer(out, x, qkv_w, z_w, b_w, a_w, conv_w, A_log, dt_bias, gate_norm_w, out_w, rec,
+                        conv_state, M_W8A8, S(stream));
+}
+
+int qh_attention_layer(float* out, const float* x, const qh_tensor* q_w, const qh_tensor* k_w,
+                       const qh_tensor* v_w, const qh_tensor* o_w, const float* q_norm, const float* k_norm,
+                       int pos, float* kcache, float* vcache, int T, void* stream) {
+  return attention_layer(out, x, q_w, k_w, v_w, o_w, q_norm, k_norm, pos, kcache, vcache, T, M_W8A16,
+                         S(stream));
+}
+int qh_attention_layer_w8a8(float* out, const float* x, const qh_tensor* q_w, const qh_tensor* k_w,
+                            const qh_tensor* v_w, const qh_tensor* o_w, const float* q_norm,
+                            const float* k_norm, int pos, float* kcache, float* vcache, int T, void* stream) {
+  return attention_layer(out, x, q_w, k_w, v_w, o_w, q_norm, k_norm, pos, kcache, vcache, T, M_W8A8,
+                         S(stream));
+}
+
+int qh_mlp_layer(float* out, const float* x, const qh_tensor* gate_w, const qh_tensor* up_w,
+                 const qh_tensor* down_w, void* stream) {
+  return mlp_layer(out, x, gate_w, up_w, down_w, M_W8A16, S(stream));
+}
+int qh_mlp_layer_w8a8(float* out, const float* x, const qh_tensor* gate_w, const qh_tensor* up_w,
+                      const qh_tensor* down_w, void* stream) {
+  return mlp_layer(out, x, gate_w, up_w, down_w, M_W8A8, S(stream));
+}
+
+int qh_quant_act(int8_t* xq, float* sx, const float* x, int n, void* stream) {
+  if (!xq || !sx || !x || n <= 0) return QH_EINVAL;
+  return hip_status(launch_quant(xq, sx, x, n, S(stream)));
+}
+
+int qh_gemv_i8_w8a8(float* y, int32_t* acc, const int8_t* w, const float* scale, const int8_t* xq,
+                    const float* sx, int out, int in, void* stream) {
+  if (!y || !w || !scale || !xq || !sx || !aligned16(w) || !aligned16(xq)) return QH_EINVAL;
+  QH_TRY(check_gemv_shape(out, in));
+  GemvArgs a;
+  a.K = in;
+  a.mode = M_W8A8;
+  a.prologue = P_LOADQ;
+  a.xq = xq;
+  a.sx = sx;
+  a.nseg = 1;
+  a.seg[0] = seg_i8(w, scale, out, 0, y, acc ? E_ACC : E_STORE);
+  a.seg[0].acc_out = acc;
+  return hip_status(launch_gemv(a, 4, S(stream)));
+}
+
+// ---- layout / synthetic weights ----
+size_t qh_blob_size(void) { return (size_t)canonical_layout().total; }
+
+size_t qh_layout_idx_text(char* buf, size_t cap) {
+  const std::string t = idx_text(canonical_layout());
+  if (buf && cap > 0) {
+    const size_t n = t.size() < cap - 1 ? t.size() : cap - 1;
+    std::memcpy(buf, t.data(), n);
+    buf[n] = '\0';
+  }
+  return t.size();
+}
+
+int qh_synth_blob(void* blob, size_t len, uint64_t seed) {
+  const Layout& L = canonical_layout();
+  if (!blob || len < L.total) return QH_EINVAL;
+  synth_blob(static_cast<uint8_t*>(blob), L, seed);
+  return QH_OK;
+}
+
+int qh_synth_fill_i8(int8_t* dst, size_t n, uint64_t key) {
+  if (!dst) return QH_EINVAL;
+  fill_i8(dst, n, key);
+  return QH_OK;
+}
+int qh_synth_fill_uniform(float* dst, size_t n, uint64_t key, float lo, float hi) {
+  if (!dst) return QH_EINVAL;
+  fill_uniform(dst, n, key, lo, hi);
+  return QH_OK;
+}
+int qh_synth_fill_normal(float* dst, size_t n, uint64_t key, float mean, float stddev) {
+  if (!dst) return QH_EINVAL;
+  fill_normal(dst, n, key, mean, stddev);
+  return QH_OK;
+}
+
+}  // extern "C"
