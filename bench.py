@@ -1,0 +1,167 @@
+#!/usr/bin/env python3
+"""Batch-1 decode throughput of the 24-layer int8 hybrid model on one MI355X.
+
+Workload ("C5"): the full Qwen3.5-0.8B-shaped model
+with seeded synthetic int8 weights in the packed pack_weights.py layout; a
+64-token seeded prompt is fed through the recurrent path (untimed), then
+`--steps` greedy decode steps are timed (default 512, so the KV cache grows to
+576).  One "step" is one decode token: embed, 24 layers, final norm, the tied
+248320x1024 int8 head and its on-device argmax, replayed as a hipGraph with
+the token fed back on the device.
+
+Prints one JSON line with tok/s, the achieved HBM bandwidth per token against
+the 8 TB/s MI355X peak, the roofline of the dominant kernel (the LM head, timed
+with HIP events on the engine stream), and the reference CPU path (the
+reference's hls/src decode top compiled natively, one core) on a bounded sample.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_GBS = 8000.0          # MI355X HBM3E, AMD published
+FLOOR_BYTES = 758_248_704  # int8 payload + scales + fp32 tensors read per token (artifacts/access.txt:1)
+HEAD_BYTES = 248320 * 1024 + 248320 * 4 + 2 * 4096   # int8 rows + scales + h + final-norm gain
+
+
+def full_bytes(T: int) -> int:
+    """Algorithmic bytes of one token with T cached positions: weights + DeltaNet
+    state r/w + conv history r/w + KV read (T+1 rows) and write."""
+    return 799_536_384 + 24_576 * (T + 1)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=512)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prompt", type=int, default=64)
+    ap.add_argument("--mode", choices=["w8a8", "w8a16"], default="w8a8")
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--cpu-tokens", type=int, default=8, help="reference CPU decode sample (tokens)")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile-steps", type=int, default=16)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build runs batch-1 decode on a single MI355X "
+              "(multi-GPU is design-only, see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import qwen_fpga_amd as q
+
+    torch.cuda.set_device(0)
+    blob = q.synth_blob(args.seed)
+    idx = q.idx_text()
+    rng = np.random.default_rng(args.seed)
+    prompt = rng.integers(0, q.VOCAB, size=args.prompt).astype(np.int32).tolist()
+    mode = q.MODE_W8A8 if args.mode == "w8a8" else q.MODE_W8A16
+    max_ctx = args.prompt + max(args.steps, args.warmup) + args.profile_steps + 2
+    eng = q.Engine(blob, idx=idx, max_ctx=max_ctx, mode=mode)
+
+    # warmup: graph instantiation + a short run from a fresh state
+    eng.reset()
+    eng.generate(prompt, args.warmup)
+    torch.cuda.synchronize()
+
+    # timed: prefill (untimed), then exactly `steps` decode steps
+    eng.reset()
+    eng.generate(prompt, 0)
+    cur = eng.last_argmax
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = eng.generate([cur], args.steps - 1)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    if len(out) != args.steps - 1:
+        print(f"generated {len(out)} of {args.steps - 1} tokens", file=sys.stderr)
+        return 1
+    dt = t1 - t0
+    tok_s = args.steps / dt
+    T0 = args.prompt
+    mean_full = sum(full_bytes(T0 + i) for i in range(args.steps)) / args.steps
+    achieved_gbs = FLOOR_BYTES * tok_s / 1e9
+
+    # dominant kernel: the LM head, HIP events on the engine stream, in-step context
+    step_ms, head_ms = eng.profile(args.profile_steps)
+    head_gbs = HEAD_BYTES / (head_ms * 1e-3) / 1e9
+
+    line = {
+        "metric": "batch-1 decode tok/s (24-layer int8) + achieved HBM GB/s vs peak",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 * dt / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8" if mode == q.MODE_W8A8 else "int8xf32",
+        "data": "synthetic (seeded random-init int8 weights in the pack_weights.py layout)",
+        "config": {
+            "workload": "C5: full 24-layer Qwen3.5-0.8B-shaped decode, batch 1, "
+                        f"{args.prompt}-token prompt then {args.steps} greedy steps (KV to "
+                        f"{args.prompt + args.steps})",
+            "act_mode": args.mode,
+            "bytes_per_token_floor": FLOOR_BYTES,
+            "bytes_per_token_full_mean": int(mean_full),
+        },
+        "achieved_hbm_gbs": round(achieved_gbs, 1),
+        "achieved_hbm_gbs_full": round(mean_full * tok_s / 1e9, 1),
+        "hbm_peak_gbs": PEAK_GBS,
+        "frac_of_roofline": round(achieved_gbs / PEAK_GBS, 4),
+        "roofline": {
+            "kernel": "head_kernel (tied 248320x1024 int8 LM head + block argmax)",
+            "bound": "hbm",
+            "achieved": round(head_gbs, 1),
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(head_gbs / PEAK_GBS, 4),
+            "traffic": None,
+            "duration_us": round(head_ms * 1e3, 2),
+            "bytes_per_launch": HEAD_BYTES,
+            "stream_step_ms": round(step_ms, 4),
+        },
+    }
+    eng.close()
+
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(blob, idx, prompt, args.cpu_tokens)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_baseline(blob, idx, prompt, ntok):
+    """The reference decode top on the host: the compiled hls/src qwen_top when
+    oracle/_ref is built, else the C restatement in reference order; one core."""
+    import oracle
+
+    toks = prompt[:ntok]
+    if oracle.ref() is not None:
+        m = oracle.RefModel(blob)
+        t0 = time.perf_counter()
+        for t in toks:
+            m.qwen_top(int(t))
+        dt = time.perf_counter() - t0
+        kind, what = "reference", "reference hls/src qwen_top compiled -O2 -ffp-contract=off (csim build)"
+    else:
+        oracle.lib().or_set_threads(1)
+        m = oracle.Model(blob, idx, len(toks) + 1)
+        t0 = time.perf_counter()
+        for t in toks:
+            m.decode_token(int(t))
+        dt = time.perf_counter() - t0
+        kind, what = "port", "oracle.c reference-order restatement, single thread"
+    return {"value": round(len(toks) / dt, 4), "unit": "tok/s", "cores": 1, "kind": kind,
+            "sample": f"{len(toks)} decode tokens of the same synthetic model from a fresh state ({what})"}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -208,6 +208,13 @@ int qh_engine_last_argmax(const qh_engine* e);
  * [1024]) without embed / final norm / head; state and pos advance as in a
  * full step.  Used for the 4-layer block configuration. */
 int qh_engine_forward_layers(qh_engine* e, int l0, int l1, float* h);
+/* Measurement hook: runs n_steps decode steps as plain stream launches (the
+ * kernels of the step graph, each fed the current token) and returns the mean
+ * step time and the mean duration of the LM-head kernel, both from HIP events
+ * on the engine stream.  Advances pos like n_steps decode_token calls. */
+int qh_engine_profile(qh_engine* e, int n_steps, float* step_ms, float* head_ms);
+/* The engine's HIP stream (a hipStream_t). */
+void* qh_engine_stream(qh_engine* e);
 /* Device pointers of engine-owned buffers (for parity checks):
  * which = 0 blob, 1 rec state [18][16][128][128], 2 conv state [18][6144][4],
  * 3 K cache [6][max_ctx][512], 4 V cache [6][max_ctx][512], 5 hidden h [1024]. */

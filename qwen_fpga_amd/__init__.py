@@ -93,6 +93,8 @@ def _lib() -> ctypes.CDLL:
             getattr(lib, n).argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_float,
                                         ctypes.c_float]
         lib.qh_synth_fill_i8.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint64]
+        lib.qh_engine_stream.restype = ctypes.c_void_p
+        lib.qh_engine_stream.argtypes = [ctypes.c_void_p]
         lib.qh_engine_device_ptr.restype = ctypes.c_void_p
         lib.qh_engine_device_ptr.argtypes = [ctypes.c_void_p, ctypes.c_int]
         _LIB = lib
@@ -377,6 +379,17 @@ class Engine:
         """Layers [l0, l1) on a device hidden vector h (torch, in place)."""
         _check(_lib().qh_engine_forward_layers(self._h, ctypes.c_int(l0), ctypes.c_int(l1),
                                                ctypes.c_void_p(_ptr(h))), "qh_engine_forward_layers")
+
+    def profile(self, n_steps: int):
+        """(mean step ms, mean LM-head kernel ms) over n_steps stream-launched steps."""
+        st, hd = ctypes.c_float(), ctypes.c_float()
+        _check(_lib().qh_engine_profile(self._h, ctypes.c_int(n_steps), ctypes.byref(st), ctypes.byref(hd)),
+               "qh_engine_profile")
+        return float(st.value), float(hd.value)
+
+    @property
+    def stream(self) -> int:
+        return int(_lib().qh_engine_stream(self._h) or 0)
 
     def device_ptr(self, which: int) -> int:
         return int(_lib().qh_engine_device_ptr(self._h, ctypes.c_int(which)) or 0)

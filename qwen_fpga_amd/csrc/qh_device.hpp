@@ -137,6 +137,17 @@ __device__ __forceinline__ int quant_one(float x, float s) {
   r = fminf(fmaxf(r, -127.0f), 127.0f);
   return (int)r;
 }
+// Same q with the quotient formed by Markstein's correction from rs = RN(1/s):
+// q0 = x*rs, r = fma(-s, q0, x), q = fma(r, rs, q0) equals RN(x/s) on this
+// domain (|x| <= amax) except for the sign of a zero quotient, which rint and
+// the int conversion erase.
+__device__ __forceinline__ int quant_one_r(float x, float s, float rs) {
+  const float q0 = x * rs;
+  const float r = __builtin_fmaf(-s, q0, x);
+  float t = __builtin_rintf(__builtin_fmaf(r, rs, q0));
+  t = fminf(fmaxf(t, -127.0f), 127.0f);
+  return (int)t;
+}
 __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
   return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
          ((uint32_t)(d & 0xff) << 24);

@@ -75,13 +75,13 @@ const float* scp(const qh_engine* e, int layer, Role r) {
   return reinterpret_cast<const float*>(e->blob + e->L->get(layer, r)->soff);
 }
 
-Seg mkseg(int kind, int epi, int rows, int batch0, float* out) {
+Seg mkseg(int kind, int epi, int rows, int batch0, float* out, int rpb = kRowsPerBatch) {
   Seg g;
   g.kind = kind;
   g.epi = epi;
   g.rows = rows;
   g.batch0 = batch0;
-  g.nbatch = (rows + kRowsPerBatch - 1) / kRowsPerBatch;
+  g.nbatch = (rows + rpb - 1) / rpb;
   g.out = out;
   return g;
 }
@@ -114,7 +114,7 @@ int enqueue_layers(qh_engine* e, int l0, int l1, bool embed, hipStream_t s) {
       a.seg[0].sw = scp(e, l, R_QKV);
       a.seg[0].c0 = f32p(e, l, R_CONV);
       a.seg[0].c2 = e->conv + (size_t)li * kConvDim * kConvK;
-      a.seg[1] = mkseg(SEG_I8, E_STORE, kZDim, a.seg[0].nbatch, e->zb);
+      a.seg[1] = mkseg(SEG_I8, E_SILU, kZDim, a.seg[0].nbatch, e->zb);   // silu(z) for the gated norm
       a.seg[1].w = i8p(e, l, R_Z);
       a.seg[1].sw = scp(e, l, R_Z);
       a.seg[2] = mkseg(SEG_F32, E_GATE_B, kLH, a.seg[1].batch0 + a.seg[1].nbatch, e->gb + 16);
@@ -141,7 +141,8 @@ int enqueue_layers(qh_engine* e, int l0, int l1, bool embed, hipStream_t s) {
       c.eps = kEps;
       c.done = done;
       c.nseg = 1;
-      c.seg[0] = mkseg(SEG_I8, E_RESID, kHidden, 0, e->h);
+      c.rows_per_batch = 4;
+      c.seg[0] = mkseg(SEG_I8, E_RESID, kHidden, 0, e->h, 4);
       c.seg[0].w = i8p(e, l, R_OUTP);
       c.seg[0].sw = scp(e, l, R_OUTP);
       QH_HIP(launch_gemv(c, 1, s));
@@ -194,7 +195,8 @@ int enqueue_layers(qh_engine* e, int l0, int l1, bool embed, hipStream_t s) {
       c.x = e->og;
       c.done = done;
       c.nseg = 1;
-      c.seg[0] = mkseg(SEG_I8, E_RESID, kHidden, 0, e->h);
+      c.rows_per_batch = 4;
+      c.seg[0] = mkseg(SEG_I8, E_RESID, kHidden, 0, e->h, 4);
       c.seg[0].w = i8p(e, l, R_OP);
       c.seg[0].sw = scp(e, l, R_OP);
       QH_HIP(launch_gemv(c, 1, s));
@@ -223,7 +225,8 @@ int enqueue_layers(qh_engine* e, int l0, int l1, bool embed, hipStream_t s) {
     dn.x = e->act;
     dn.done = done;
     dn.nseg = 1;
-    dn.seg[0] = mkseg(SEG_I8, E_RESID, kHidden, 0, e->h);
+    dn.rows_per_batch = 4;
+    dn.seg[0] = mkseg(SEG_I8, E_RESID, kHidden, 0, e->h, 4);
     dn.seg[0].w = i8p(e, l, R_DOWN);
     dn.seg[0].sw = scp(e, l, R_DOWN);
     QH_HIP(launch_gemv(dn, 1, s));
@@ -233,7 +236,8 @@ int enqueue_layers(qh_engine* e, int l0, int l1, bool embed, hipStream_t s) {
 
 // One full decode step (qwen_top): embed, 24 layers, final norm, tied head,
 // argmax (+ pos), optionally the generation bookkeeping.
-int enqueue_step(qh_engine* e, bool with_logits, bool advance, hipStream_t s) {
+int enqueue_step(qh_engine* e, bool with_logits, bool advance, hipStream_t s,
+                 hipEvent_t head_t0 = nullptr, hipEvent_t head_t1 = nullptr) {
   QH_TRY(enqueue_layers(e, 0, kLayers, true, s));
   HeadArgs hd;
   hd.h = e->h;
@@ -246,7 +250,9 @@ int enqueue_step(qh_engine* e, bool with_logits, bool advance, hipStream_t s) {
   hd.part_val = e->part_val;
   hd.part_idx = e->part_idx;
   hd.done = &e->ctl->done;
+  if (head_t0) QH_HIP(hipEventRecord(head_t0, s));
   QH_HIP(launch_head(hd, e->head_grid, s));
+  if (head_t1) QH_HIP(hipEventRecord(head_t1, s));
   QH_HIP(launch_argmax(e->part_val, e->part_idx, e->head_grid, e->ctl, nullptr, s));
   if (advance) QH_HIP(launch_advance(e->ctl, e->prompt_dev, e->out_dev, s));
   return QH_OK;
@@ -502,6 +508,45 @@ int qh_engine_forward_layers(qh_engine* e, int l0, int l1, float* h) {
   e->host_pos += 1;
   return QH_OK;
 }
+
+int qh_engine_profile(qh_engine* e, int n_steps, float* step_ms, float* head_ms) {
+  if (!e || n_steps < 1 || !step_ms || !head_ms) return QH_EINVAL;
+  if ((long)e->host_pos + n_steps > e->max_ctx) return QH_ERANGE;
+  hipStream_t s = e->stream;
+  hipEvent_t a = nullptr, b = nullptr, h0 = nullptr, h1 = nullptr;
+  int st = QH_OK;
+  float tot_head = 0.0f, tot = 0.0f;
+  if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess || hipEventCreate(&h0) != hipSuccess ||
+      hipEventCreate(&h1) != hipSuccess) {
+    st = QH_ENOMEM;
+  }
+  for (int i = 0; st == QH_OK && i < n_steps; ++i) {
+    st = hip_status(launch_set_int(&e->ctl->done, 0, s));
+    if (st == QH_OK) st = hip_status(hipEventRecord(a, s));
+    if (st == QH_OK) st = enqueue_step(e, false, false, s, h0, h1);
+    if (st == QH_OK) st = hip_status(hipEventRecord(b, s));
+    if (st == QH_OK) st = hip_status(hipEventSynchronize(b));
+    float t = 0.0f, th = 0.0f;
+    if (st == QH_OK) st = hip_status(hipEventElapsedTime(&t, a, b));
+    if (st == QH_OK) st = hip_status(hipEventElapsedTime(&th, h0, h1));
+    tot += t;
+    tot_head += th;
+  }
+  if (a) (void)hipEventDestroy(a);
+  if (b) (void)hipEventDestroy(b);
+  if (h0) (void)hipEventDestroy(h0);
+  if (h1) (void)hipEventDestroy(h1);
+  if (st != QH_OK) return st;
+  StepCtl c;
+  QH_HIP(hipMemcpy(&c, e->ctl, sizeof c, hipMemcpyDeviceToHost));
+  e->host_pos = c.pos;
+  e->last_argmax = c.argmax;
+  *step_ms = tot / n_steps;
+  *head_ms = tot_head / n_steps;
+  return QH_OK;
+}
+
+void* qh_engine_stream(qh_engine* e) { return e ? (void*)e->stream : nullptr; }
 
 void* qh_engine_device_ptr(qh_engine* e, int which) {
   if (!e) return nullptr;

@@ -86,20 +86,86 @@ __device__ __forceinline__ float seg_scale(const Seg& g, int row) {
   return g.sw[row];
 }
 
-// Row-batch epilogue: lane l holds the result y of row (l >> 3) & 7 of the batch.
-__device__ __forceinline__ void gemv_epilogue(const Seg& g, int lane, int myrow, float y, int acci) {
-  if (g.epi == E_SWIGLU) {   // pair rows: even = gate i, odd = up i (mlp.hpp:17)
-    const float yo = __shfl_xor(y, 8, 64);
-    if ((lane & 15) == 0 && myrow < g.rows) g.out[myrow >> 1] = dev_silu(y) * yo;
+// Transposed xor-butterfly over R rows (R = 1, 2, 4, 8): at offsets 32, 16, ...
+// each lane keeps half of its rows and receives its partner's other half; the
+// remaining offsets finish the tree.  Lane l ends with row (l >> (6 - log2 R))
+// & (R - 1).  Per row this is the 64-lane xor tree of the C16 order.
+template <int R, typename T>
+__device__ __forceinline__ T reduce_rows(T v[R], int lane) {
+  int off = 32;
+#pragma unroll
+  for (int n = R; n > 1; n >>= 1) {
+    const bool up = (lane & off) != 0;
+#pragma unroll
+    for (int i = 0; i < n / 2; ++i) {
+      const T send = up ? v[i] : v[i + n / 2];
+      const T keep = up ? v[i + n / 2] : v[i];
+      v[i] = keep + __shfl_xor(send, off, 64);
+    }
+    off >>= 1;
+  }
+  T r = v[0];
+#pragma unroll
+  for (int o = 64 / R / 2; o >= 1; o >>= 1) r = r + __shfl_xor(r, o, 64);
+  return r;
+}
+template <int R>
+__device__ __forceinline__ int row_of_lane(int lane) {
+  return R == 1 ? 0 : (lane >> (R == 8 ? 3 : R == 4 ? 4 : 5)) & (R - 1);
+}
+
+// Per-row epilogue inputs, loaded by the writer lanes at kernel start.
+struct EpiAux {
+  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;   // conv state cols 1..3 | residual | A_log
+  float w0 = 0.0f, w1 = 0.0f, w2 = 0.0f, w3 = 0.0f;   // conv taps | dt_bias
+};
+__device__ __forceinline__ void epi_prefetch(const Seg& g, int myrow, EpiAux& x) {
+  if (myrow >= g.rows) return;
+  switch (g.epi) {
+    case E_RESID:
+      x.a0 = g.out[myrow];
+      break;
+    case E_GATE_A:
+      x.a0 = g.c0[myrow];
+      x.w0 = g.c1[myrow];
+      break;
+    case E_CONV: {
+      const float4 st = *reinterpret_cast<const float4*>(g.c2 + (size_t)myrow * 4);
+      const float4 w = *reinterpret_cast<const float4*>(g.c0 + (size_t)myrow * 4);
+      x.a1 = st.y;
+      x.a2 = st.z;
+      x.a3 = st.w;
+      x.w0 = w.x;
+      x.w1 = w.y;
+      x.w2 = w.z;
+      x.w3 = w.w;
+      break;
+    }
+    default:
+      break;
+  }
+}
+
+// Row-batch epilogue: the writer lane of each row stores its result y.
+template <int R>
+__device__ __forceinline__ void gemv_epilogue(const Seg& g, int lane, int myrow, float y, int acci,
+                                              const EpiAux& x) {
+  constexpr int LPR = 64 / R;   // lanes holding one row
+  if (g.epi == E_SWIGLU) {      // pair rows: even = gate i, odd = up i (mlp.hpp:17)
+    const float yo = __shfl_xor(y, LPR, 64);
+    if ((lane & (2 * LPR - 1)) == 0 && myrow < g.rows) g.out[myrow >> 1] = dev_silu(y) * yo;
     return;
   }
-  if ((lane & 7) != 0 || myrow >= g.rows) return;
+  if ((lane & (LPR - 1)) != 0 || myrow >= g.rows) return;
   switch (g.epi) {
     case E_STORE:
       g.out[myrow] = y;
       break;
+    case E_SILU:   // silu(z) for the gated norm (norm.hpp:32)
+      g.out[myrow] = dev_silu(y);
+      break;
     case E_RESID:
-      g.out[myrow] = g.out[myrow] + y;
+      g.out[myrow] = x.a0 + y;
       break;
     case E_ACC:
       g.out[myrow] = y;
@@ -109,21 +175,15 @@ __device__ __forceinline__ void gemv_epilogue(const Seg& g, int lane, int myrow,
       g.out[myrow] = dev_sigmoid(y);
       break;
     case E_GATE_A:
-      g.out[myrow] = -dev_expf(g.c0[myrow]) * dev_softplus(y + g.c1[myrow]);
+      g.out[myrow] = -dev_expf(x.a0) * dev_softplus(y + x.w0);
       break;
-    case E_CONV: {   // conv1d.hpp:22-36
-      float* st = g.c2 + (size_t)myrow * 4;
-      const float* w = g.c0 + (size_t)myrow * 4;
-      const float w0 = st[1], w1 = st[2], w2 = st[3], w3 = y;
+    case E_CONV: {   // conv1d.hpp:22-36: window = state cols 1..3 + new sample
       float acc = 0.0f;
-      acc = acc + w0 * w[0];
-      acc = acc + w1 * w[1];
-      acc = acc + w2 * w[2];
-      acc = acc + w3 * w[3];
-      st[0] = w0;
-      st[1] = w1;
-      st[2] = w2;
-      st[3] = w3;
+      acc = acc + x.a1 * x.w0;
+      acc = acc + x.a2 * x.w1;
+      acc = acc + x.a3 * x.w2;
+      acc = acc + y * x.w3;
+      *reinterpret_cast<float4*>(g.c2 + (size_t)myrow * 4) = make_float4(x.a1, x.a2, x.a3, y);
       g.out[myrow] = dev_silu(acc);
       break;
     }
@@ -132,16 +192,54 @@ __device__ __forceinline__ void gemv_epilogue(const Seg& g, int lane, int myrow,
   }
 }
 
-template <int NCH, int MODE, int PRO>
+template <int NCH, int R>
+__device__ __forceinline__ void load_batch(const Seg& g, int row0, int K, int nchunk, int lane,
+                                           uint32_t (&w)[NCH][R][4]) {
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int c = lane + 64 * j;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (c < nchunk && row0 + r < g.rows) {
+        load16b(seg_row(g, row0 + r, K) + 16 * c, w[j][r]);
+      } else {
+        w[j][r][0] = w[j][r][1] = w[j][r][2] = w[j][r][3] = 0u;
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ int seg_of(const GemvArgs& a, int b) {
+  int si = 0;
+  while (si + 1 < a.nseg && b >= a.seg[si + 1].batch0) ++si;
+  return si;
+}
+
+template <int NCH, int MODE, int PRO, int R>
 __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
   if (a.done != nullptr && *a.done != 0) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwv = blockDim.x >> 6;
   const int K = a.K, nchunk = K >> 4;
+  const int total = a.seg[a.nseg - 1].batch0 + a.seg[a.nseg - 1].nbatch;
+  const int stride = gridDim.x * nwv;
+  int b = blockIdx.x * nwv + wave;
+
+  // ---------------- 1. weights and epilogue inputs of the first batch in flight first
+  uint32_t w[NCH][R][4];
+  EpiAux aux;
+  int si = 0;
+  if (b < total) {
+    si = seg_of(a, b);
+    const Seg& g = a.seg[si];
+    const int row0 = (b - g.batch0) * R;
+    if (g.kind != SEG_F32) load_batch<NCH, R>(g, row0, K, nchunk, lane, w);
+    epi_prefetch(g, row0 + row_of_lane<R>(lane), aux);
+  }
+
+  // ---------------- 2. prologue: this lane's chunks c = lane + 64 j of x
   float xv[NCH][16];     // fp32 activation (W8A16) / dequantized q*s (W8A8)
   uint32_t xq[NCH][4];   // int8 activation (W8A8)
   float xs = 1.0f;       // activation scale (W8A8)
-
-  // ---------------- prologue: this lane's chunks c = lane + 64 j of x
   if constexpr (PRO == P_LOADQ) {
     xs = *a.sx;
 #pragma unroll
@@ -156,6 +254,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
       for (int e = 0; e < 16; ++e) xv[j][e] = i8_at(xq[j], e) * xs;
     }
   } else {
+    float nwv16[NCH][16];
+    if constexpr (PRO == P_NORM || PRO == P_GATED) {
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int c = lane + 64 * j;
+        if (c < nchunk) load16f(a.nw + (PRO == P_GATED ? ((16 * c) & 127) : 16 * c), nwv16[j]);
+      }
+    }
     if (PRO == P_NORM && a.emb != nullptr) {   // embed_row (gemv.hpp:76-84)
       const int tok = *a.tok;
       const int8_t* er = a.emb + (size_t)tok * K;
@@ -164,10 +270,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
       for (int j = 0; j < NCH; ++j) {
         const int c = lane + 64 * j;
         if (c < nchunk) {
-          uint32_t w[4];
-          load16b(er + 16 * c, w);
+          uint32_t t[4];
+          load16b(er + 16 * c, t);
 #pragma unroll
-          for (int e = 0; e < 16; ++e) xv[j][e] = i8_at(w, e) * es;
+          for (int e = 0; e < 16; ++e) xv[j][e] = i8_at(t, e) * es;
           if (a.h_out != nullptr && blockIdx.x == 0 && threadIdx.x < 64) store16f(a.h_out + 16 * c, xv[j]);
         } else {
 #pragma unroll
@@ -194,29 +300,21 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
       ss = xor_sum<64>(ss);
       const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
 #pragma unroll
-      for (int j = 0; j < NCH; ++j) {
-        const int c = lane + 64 * j;
-        if (c < nchunk) {
-          float w[16];
-          load16f(a.nw + 16 * c, w);
+      for (int j = 0; j < NCH; ++j)
+        if (lane + 64 * j < nchunk)
 #pragma unroll
-          for (int e = 0; e < 16; ++e) xv[j][e] = (xv[j][e] * inv) * (1.0f + w[e]);
-        }
-      }
-    } else if constexpr (PRO == P_GATED) {   // heads of 128 = groups of 8 lanes
+          for (int e = 0; e < 16; ++e) xv[j][e] = (xv[j][e] * inv) * (1.0f + nwv16[j][e]);
+    } else if constexpr (PRO == P_GATED) {   // heads of 128 = groups of 8 lanes; z holds silu(z)
+      float zs[NCH][16];
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) load16f(a.z + 16 * (lane + 64 * j), zs[j]);
 #pragma unroll
       for (int j = 0; j < NCH; ++j) {
-        const int c = lane + 64 * j;
         float ss = dot16_f32(xv[j], xv[j], 0.0f);
         ss = xor_sum<8>(ss);
         const float inv = 1.0f / sqrtf(ss / 128.0f + a.eps);
-        if (c < nchunk) {
-          float w[16], z[16];
-          load16f(a.nw + ((16 * c) & 127), w);
-          load16f(a.z + 16 * c, z);
 #pragma unroll
-          for (int e = 0; e < 16; ++e) xv[j][e] = ((xv[j][e] * inv) * w[e]) * dev_silu(z[e]);
-        }
+        for (int e = 0; e < 16; ++e) xv[j][e] = ((xv[j][e] * inv) * nwv16[j][e]) * zs[j][e];
       }
     }
     if constexpr (MODE == M_W8A8) {   // _qa (golden/model.py:37-45)
@@ -227,12 +325,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
         for (int e = 0; e < 16; ++e) am = fmaxf(am, fabsf(xv[j][e]));
       am = xor_max<64>(am);
       xs = quant_scale(am);
+      const float rs = 1.0f / xs;
 #pragma unroll
       for (int j = 0; j < NCH; ++j) {
         int q[16];
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          q[e] = quant_one(xv[j][e], xs);
+          q[e] = quant_one_r(xv[j][e], xs, rs);
           xv[j][e] = (float)q[e] * xs;
         }
 #pragma unroll
@@ -241,103 +340,103 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
     }
   }
 
-  // ---------------- row batches
-  const int total = a.seg[a.nseg - 1].batch0 + a.seg[a.nseg - 1].nbatch;
-  for (int b = blockIdx.x * nwv + wave; b < total; b += gridDim.x * nwv) {
-    int si = 0;
-    while (si + 1 < a.nseg && b >= a.seg[si + 1].batch0) ++si;
+  // ---------------- 3. row batches (the next batch's loads overlap this batch's reduction)
+  for (; b < total; b += stride) {
     const Seg& g = a.seg[si];
-    const int row0 = (b - g.batch0) * kRowsPerBatch;
-    const int myrow = row0 + ((lane >> 3) & 7);
+    const int row0 = (b - g.batch0) * R;
+    const int myrow = row0 + row_of_lane<R>(lane);
     float y = 0.0f;
     int acci = 0;
+    float pf[R];
+    int pi[R];
     if (g.kind == SEG_F32) {   // fp32 weights (gemv.hpp:46-59)
-      float p[8];
 #pragma unroll
-      for (int r = 0; r < 8; ++r) p[r] = 0.0f;
+      for (int r = 0; r < R; ++r) pf[r] = 0.0f;
 #pragma unroll
       for (int j = 0; j < NCH; ++j) {
         const int c = lane + 64 * j;
         if (c < nchunk) {
 #pragma unroll
-          for (int r = 0; r < 8; ++r) {
+          for (int r = 0; r < R; ++r) {
             if (row0 + r < g.rows) {
-              float w[16];
-              load16f(g.wf + (size_t)(row0 + r) * K + 16 * c, w);
-              p[r] = dot16_f32(w, xv[j], p[r]);
+              float wf[16];
+              load16f(g.wf + (size_t)(row0 + r) * K + 16 * c, wf);
+              pf[r] = dot16_f32(wf, xv[j], pf[r]);
             }
           }
         }
       }
-      y = reduce8(p, lane);
     } else if constexpr (MODE == M_W8A16) {   // int8 x fp32 (gemv.hpp:28-42)
-      float p[8];
 #pragma unroll
-      for (int r = 0; r < 8; ++r) p[r] = 0.0f;
+      for (int r = 0; r < R; ++r) pf[r] = 0.0f;
 #pragma unroll
-      for (int j = 0; j < NCH; ++j) {
-        const int c = lane + 64 * j;
-        if (c < nchunk) {
-          uint32_t w[8][4];
+      for (int j = 0; j < NCH; ++j)
+        if (lane + 64 * j < nchunk)
 #pragma unroll
-          for (int r = 0; r < 8; ++r) {
-            if (row0 + r < g.rows) {
-              load16b(seg_row(g, row0 + r, K) + 16 * c, w[r]);
-            } else {
-              w[r][0] = w[r][1] = w[r][2] = w[r][3] = 0u;
-            }
-          }
+          for (int r = 0; r < R; ++r) pf[r] = dot16_i8f(w[j][r], xv[j], pf[r]);
+    } else {   // int8 x int8 -> int32 (export_gemv_tv.py:298)
 #pragma unroll
-          for (int r = 0; r < 8; ++r) p[r] = dot16_i8f(w[r], xv[j], p[r]);
-        }
-      }
-      y = reduce8(p, lane);
-      if (myrow < g.rows) y = y * seg_scale(g, myrow);
-    } else {   // int8 x int8 -> int32, dequant float(acc)*sx*sw (export_gemv_tv.py:298-299)
-      int p[8];
+      for (int r = 0; r < R; ++r) pi[r] = 0;
 #pragma unroll
-      for (int r = 0; r < 8; ++r) p[r] = 0;
+      for (int j = 0; j < NCH; ++j)
 #pragma unroll
-      for (int j = 0; j < NCH; ++j) {
-        const int c = lane + 64 * j;
-        if (c < nchunk) {
-          uint32_t w[8][4];
-#pragma unroll
-          for (int r = 0; r < 8; ++r) {
-            if (row0 + r < g.rows) {
-              load16b(seg_row(g, row0 + r, K) + 16 * c, w[r]);
-            } else {
-              w[r][0] = w[r][1] = w[r][2] = w[r][3] = 0u;
-            }
-          }
-#pragma unroll
-          for (int r = 0; r < 8; ++r) p[r] = dot16_i8i8(w[r], xq[j], p[r]);
-        }
-      }
-      acci = reduce8(p, lane);
-      if (myrow < g.rows) y = ((float)acci * xs) * seg_scale(g, myrow);
+        for (int r = 0; r < R; ++r) pi[r] = dot16_i8i8(w[j][r], xq[j], pi[r]);
     }
-    gemv_epilogue(g, lane, myrow, y, acci);
+    // issue the next batch's loads before reducing this one
+    const int bn = b + stride;
+    int sin = si;
+    EpiAux auxn;
+    if (bn < total) {
+      sin = seg_of(a, bn);
+      const Seg& gn = a.seg[sin];
+      const int rn = (bn - gn.batch0) * R;
+      if (gn.kind != SEG_F32) load_batch<NCH, R>(gn, rn, K, nchunk, lane, w);
+      epi_prefetch(gn, rn + row_of_lane<R>(lane), auxn);
+    }
+    if (g.kind == SEG_F32 || MODE == M_W8A16) {
+      y = reduce_rows<R>(pf, lane);
+      if (g.kind != SEG_F32 && myrow < g.rows) y = y * seg_scale(g, myrow);
+    } else {
+      acci = reduce_rows<R>(pi, lane);
+      if (myrow < g.rows) y = ((float)acci * xs) * seg_scale(g, myrow);   // float(acc)*sx*sw
+    }
+    gemv_epilogue<R>(g, lane, myrow, y, acci, aux);
+    si = sin;
+    aux = auxn;
   }
 }
 
-template <int NCH, int MODE>
+template <int NCH, int MODE, int R>
 static void launch_gemv_pro(const GemvArgs& a, int grid, dim3 blk, hipStream_t s) {
   switch (a.prologue) {
-    case P_NORM: gemv_kernel<NCH, MODE, P_NORM><<<grid, blk, 0, s>>>(a); break;
-    case P_GATED: gemv_kernel<NCH, MODE, P_GATED><<<grid, blk, 0, s>>>(a); break;
-    case P_LOADQ: gemv_kernel<NCH, MODE, P_LOADQ><<<grid, blk, 0, s>>>(a); break;
-    default: gemv_kernel<NCH, MODE, P_LOAD><<<grid, blk, 0, s>>>(a); break;
+    case P_NORM: gemv_kernel<NCH, MODE, P_NORM, R><<<grid, blk, 0, s>>>(a); break;
+    case P_GATED: gemv_kernel<NCH, MODE, P_GATED, R><<<grid, blk, 0, s>>>(a); break;
+    case P_LOADQ:
+      if constexpr (MODE == M_W8A8) gemv_kernel<NCH, MODE, P_LOADQ, R><<<grid, blk, 0, s>>>(a);
+      break;
+    default: gemv_kernel<NCH, MODE, P_LOAD, R><<<grid, blk, 0, s>>>(a); break;
   }
 }
-template <int NCH>
+template <int NCH, int R>
 static void launch_gemv_mode(const GemvArgs& a, int grid, dim3 blk, hipStream_t s) {
   if (a.mode == M_W8A8)
-    launch_gemv_pro<NCH, M_W8A8>(a, grid, blk, s);
+    launch_gemv_pro<NCH, M_W8A8, R>(a, grid, blk, s);
   else
-    launch_gemv_pro<NCH, M_W8A16>(a, grid, blk, s);
+    launch_gemv_pro<NCH, M_W8A16, R>(a, grid, blk, s);
+}
+template <int R>
+static hipError_t launch_gemv_r(const GemvArgs& a, int grid, dim3 blk, hipStream_t s) {
+  switch ((a.K + 1023) / 1024) {
+    case 1: launch_gemv_mode<1, R>(a, grid, blk, s); break;
+    case 2: launch_gemv_mode<2, R>(a, grid, blk, s); break;
+    case 3: launch_gemv_mode<3, R>(a, grid, blk, s); break;
+    case 4: launch_gemv_mode<4, R>(a, grid, blk, s); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
+// Rows per batch (a.rows_per_batch) must match how the segment batches were counted.
 hipError_t launch_gemv(const GemvArgs& a, int waves_per_block, hipStream_t s) {
   if (a.nseg < 1 || a.nseg > 4 || waves_per_block < 1 || waves_per_block > 4) return hipErrorInvalidValue;
   if (a.prologue == P_LOADQ && a.mode != M_W8A8) return hipErrorInvalidValue;
@@ -345,14 +444,11 @@ hipError_t launch_gemv(const GemvArgs& a, int waves_per_block, hipStream_t s) {
   const int total = a.seg[a.nseg - 1].batch0 + a.seg[a.nseg - 1].nbatch;
   const int grid = (total + waves_per_block - 1) / waves_per_block;
   const dim3 blk(64 * waves_per_block);
-  switch ((a.K + 1023) / 1024) {
-    case 1: launch_gemv_mode<1>(a, grid, blk, s); break;
-    case 2: launch_gemv_mode<2>(a, grid, blk, s); break;
-    case 3: launch_gemv_mode<3>(a, grid, blk, s); break;
-    case 4: launch_gemv_mode<4>(a, grid, blk, s); break;
+  switch (a.rows_per_batch) {
+    case 4: return launch_gemv_r<4>(a, grid, blk, s);
+    case 8: return launch_gemv_r<8>(a, grid, blk, s);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 // ===========================================================================
@@ -370,31 +466,40 @@ __device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
 __global__ __launch_bounds__(256) void head_kernel(const HeadArgs a) {
   if (a.done != nullptr && *a.done != 0) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwv = blockDim.x >> 6;
-  float xv[16];
+  const int total = a.rows / kRowsPerBatch;
+  const int stride = gridDim.x * nwv;
+  int b = blockIdx.x * nwv + wave;
+  const int rl = (lane >> 3) & 7;
+  uint32_t w[8][4];
+  float sc = 0.0f;
+  if (b < total) {   // first batch in flight before the norm prologue
+#pragma unroll
+    for (int r = 0; r < 8; ++r) load16b(a.w + (size_t)(b * 8 + r) * 1024 + 16 * lane, w[r]);
+    sc = a.sw[b * 8 + rl];
+  }
+  float xv[16], nw[16];
   load16f(a.h + 16 * lane, xv);
+  load16f(a.nw + 16 * lane, nw);
   float ss = dot16_f32(xv, xv, 0.0f);
   ss = xor_sum<64>(ss);
   const float inv = 1.0f / sqrtf(ss / 1024.0f + a.eps);
-  {
-    float w[16];
-    load16f(a.nw + 16 * lane, w);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) xv[e] = (xv[e] * inv) * (1.0f + w[e]);
-  }
+  for (int e = 0; e < 16; ++e) xv[e] = (xv[e] * inv) * (1.0f + nw[e]);
   float bv = -1e30f;
   int bi = 0;
-  const int total = a.rows / kRowsPerBatch;
-  for (int b = blockIdx.x * nwv + wave; b < total; b += gridDim.x * nwv) {
-    const int row0 = b * kRowsPerBatch;
-    uint32_t w[8][4];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) load16b(a.w + (size_t)(row0 + r) * 1024 + 16 * lane, w[r]);
+  for (; b < total; b += stride) {
     float p[8];
 #pragma unroll
     for (int r = 0; r < 8; ++r) p[r] = dot16_i8f(w[r], xv, 0.0f);
-    const float y0 = reduce8(p, lane);
-    const int row = row0 + ((lane >> 3) & 7);
-    const float y = y0 * a.sw[row];
+    const float scur = sc;
+    const int bn = b + stride;
+    if (bn < total) {   // next batch in flight during the reduction
+#pragma unroll
+      for (int r = 0; r < 8; ++r) load16b(a.w + (size_t)(bn * 8 + r) * 1024 + 16 * lane, w[r]);
+      sc = a.sw[bn * 8 + rl];
+    }
+    const float y = reduce8(p, lane) * scur;
+    const int row = b * 8 + rl;
     if ((lane & 7) == 0) {
       if (a.logits != nullptr) a.logits[row] = y;
       better(bv, bi, y, row);
@@ -506,41 +611,44 @@ __global__ __launch_bounds__(256) void deltanet_kernel(const DnArgs a) {
   __shared__ float qs[128], ks[128];
   __shared__ float part[8][32];
   __shared__ float dl[32];
+  const int vl = t & 31, kg = t >> 5, v = vq * 32 + vl;
+  float* Sh = a.S + (size_t)h * 128 * 128;
+  float s[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s[i] = Sh[(kg * 16 + i) * 128 + v];   // state tile in flight first
+  const float g = a.gb[h], beta = a.gb[16 + h];
+  const float vv = a.convd[4096 + h * 128 + v];
   if (wave < 2) {   // wave 0: q, wave 1: k; lanes 0..7 hold 16 elements each
     const float* src = a.convd + (wave == 0 ? 0 : 2048) + h * 128;
-    float v[16];
+    float x[16];
     float ss = 0.0f;
     if (lane < 8) {
-      load16f(src + 16 * lane, v);
-      ss = dot16_f32(v, v, 0.0f);
+      load16f(src + 16 * lane, x);
+      ss = dot16_f32(x, x, 0.0f);
     } else {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) v[e] = 0.0f;
+      for (int e = 0; e < 16; ++e) x[e] = 0.0f;
     }
     if (a.normalize) {
       ss = xor_sum<8>(ss);
       const float inv = 1.0f / sqrtf(ss + 1e-6f);   // deltanet.hpp:134
 #pragma unroll
-      for (int e = 0; e < 16; ++e) v[e] = v[e] * inv;
+      for (int e = 0; e < 16; ++e) x[e] = x[e] * inv;
       if (wave == 0) {
         const float sc = 1.0f / sqrtf(128.0f);   // deltanet.hpp:168-169
 #pragma unroll
-        for (int e = 0; e < 16; ++e) v[e] = v[e] * sc;
+        for (int e = 0; e < 16; ++e) x[e] = x[e] * sc;
       }
     }
-    if (lane < 8) store16f((wave == 0 ? qs : ks) + 16 * lane, v);
+    if (lane < 8) store16f((wave == 0 ? qs : ks) + 16 * lane, x);
   }
   __syncthreads();
-  const int vl = t & 31, kg = t >> 5, v = vq * 32 + vl;
-  const float g = a.gb[h], beta = a.gb[16 + h];
   const float gexp = dev_expf(g);
-  float* Sh = a.S + (size_t)h * 128 * 128;
-  float s[16];
   float p = 0.0f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {   // sweep A
     const int k = kg * 16 + i;
-    s[i] = Sh[k * 128 + v] * gexp;
+    s[i] = s[i] * gexp;
     p = p + s[i] * ks[k];
   }
   part[kg][vl] = p;
@@ -553,7 +661,6 @@ __global__ __launch_bounds__(256) void deltanet_kernel(const DnArgs a) {
     for (int off = 4; off >= 1; off >>= 1)
 #pragma unroll
       for (int gi = 0; gi < off; ++gi) pp[gi] = pp[gi] + pp[gi + off];
-    const float vv = a.convd[4096 + h * 128 + v];
     dl[vl] = (vv - pp[0]) * beta;
   }
   __syncthreads();
@@ -629,6 +736,19 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
   const float* sn = cs + 32;
   __shared__ float sc[4][64];
   __shared__ float pp[4][64];
+  const int t0 = s * kAttnSplit;
+  // cached K rows of this wave's 16 positions in flight first (slot T is written below)
+  float kreg[4][16];
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int tp = t0 + 16 * wave + 4 * it + pg;
+    if (tp < T) {
+      load16f(a.kc + (size_t)tp * 512 + j * 256 + 16 * g16, kreg[it]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) kreg[it][e] = 0.0f;
+    }
+  }
   float q[4][16];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -638,7 +758,6 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
     load16f(a.qn + 16 * g16, w);
     qk_norm_rope(q[i], w, a.eps, g16, cs, sn);
   }
-  const int t0 = s * kAttnSplit;
   if (T / kAttnSplit == s) {   // owner of slot T (attention.hpp:46-54)
     if (wave == 0) {
       float k[16], w[16], v[16];
@@ -652,22 +771,17 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
       }
     }
     __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 4; ++it)
+      if (t0 + 16 * wave + 4 * it + pg == T) load16f(a.kc + (size_t)T * 512 + j * 256 + 16 * g16, kreg[it]);
   }
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int tl = 16 * wave + 4 * it + pg;   // position within the split
-    const int tp = t0 + tl;
-    const bool valid = tp < Tn;
-    float k[16];
-    if (valid) {
-      load16f(a.kc + (size_t)tp * 512 + j * 256 + 16 * g16, k);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) k[e] = 0.0f;
-    }
+    const bool valid = t0 + tl < Tn;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float d = dot16_f32(q[i], k, 0.0f);
+      float d = dot16_f32(q[i], kreg[it], 0.0f);
       d = xor_sum<16>(d);
       if (g16 == 0) sc[i][tl] = valid ? d * 0.0625f : -__builtin_inff();
     }

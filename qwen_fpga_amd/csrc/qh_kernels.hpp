@@ -6,7 +6,7 @@
 
 namespace qh {
 
-constexpr int kRowsPerBatch = 8;     // rows one wave reduces together
+constexpr int kRowsPerBatch = 8;     // rows one wave reduces together (LM head, large GEMVs)
 constexpr int kAttnSplit = 64;       // positions per attention split
 constexpr int kDnVQuarters = 4;      // DeltaNet workgroups per head (32 v columns each)
 
@@ -19,11 +19,13 @@ enum Epi : int {
   E_GATE_A = 4,  // out[row] = -exp(A_log)*softplus(y+dt_bias) (g, deltanet.hpp:165)
   E_SWIGLU = 5,  // pair rows (gate i, up i): out[i] = silu(g)*u (mlp.hpp:17)
   E_ACC = 6,     // out[row] = y and acc_out[row] = int32 accumulator (W8A8 op)
+  E_SILU = 7,    // out[row] = silu(y)  (the gated norm's silu(z), norm.hpp:32)
 };
 enum Prologue : int {
   P_LOAD = 0,    // x[K] fp32 as given
   P_NORM = 1,    // rmsnorm(x, nw) with (1+w) (norm.hpp:13-20); optional embed row first
-  P_GATED = 2,   // per-head rmsnorm_gated(o, nw, z) over 16 x 128 (deltanet.hpp:177-179)
+  P_GATED = 2,   // per-head rmsnorm_gated(o, nw, z) over 16 x 128 (deltanet.hpp:177-179);
+                 // z holds silu(z) already (E_SILU of the producing GEMV)
   P_LOADQ = 3,   // int8 xq[K] + scale sx given (W8A8 op)
 };
 enum Mode : int { M_W8A16 = 0, M_W8A8 = 1 };
@@ -45,6 +47,7 @@ struct Seg {
 
 struct GemvArgs {
   int K = 0, mode = M_W8A16, prologue = P_LOAD;
+  int rows_per_batch = 8;       // 4 or 8 rows reduced together per wave
   const float* x = nullptr;     // P_LOAD / P_NORM input, P_GATED o
   const float* nw = nullptr;    // P_NORM [K] gain, P_GATED [128] gain
   const float* z = nullptr;     // P_GATED gate input [2048]

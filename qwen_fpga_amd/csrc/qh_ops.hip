@@ -59,13 +59,14 @@ bool tensor_f32(const qh_tensor* t, int out, int in) {
   return t && t->w_f32 && t->out == out && t->in == in && aligned16(t->w_f32);
 }
 
-Seg seg_i8(const int8_t* w, const float* sw, int rows, int batch0, float* out, int epi) {
+Seg seg_i8(const int8_t* w, const float* sw, int rows, int batch0, float* out, int epi,
+           int rpb = kRowsPerBatch) {
   Seg g;
   g.kind = SEG_I8;
   g.epi = epi;
   g.batch0 = batch0;
   g.rows = rows;
-  g.nbatch = (rows + kRowsPerBatch - 1) / kRowsPerBatch;
+  g.nbatch = (rows + rpb - 1) / rpb;
   g.w = w;
   g.sw = sw;
   g.out = out;
@@ -106,7 +107,7 @@ int deltanet_layer(float* out, const float* x, const qh_tensor* qkv_w, const qh_
   a.seg[0].c0 = conv_w;
   a.seg[0].c2 = conv_state;
   b0 += a.seg[0].nbatch;
-  a.seg[1] = seg_i8(z_w->w_i8, z_w->scale, kZDim, b0, zb, E_STORE);
+  a.seg[1] = seg_i8(z_w->w_i8, z_w->scale, kZDim, b0, zb, E_SILU);   // silu(z) for the gated norm
   b0 += a.seg[1].nbatch;
   Seg gbeta;
   gbeta.kind = SEG_F32;
@@ -141,7 +142,8 @@ int deltanet_layer(float* out, const float* x, const qh_tensor* qkv_w, const qh_
   c.nw = gate_norm_w;
   c.z = zb;
   c.nseg = 1;
-  c.seg[0] = seg_i8(out_w->w_i8, out_w->scale, kHidden, 0, out, E_STORE);
+  c.rows_per_batch = 4;
+  c.seg[0] = seg_i8(out_w->w_i8, out_w->scale, kHidden, 0, out, E_STORE, 4);
   QH_HIP(launch_gemv(c, 1, s));
   return QH_OK;
 }
@@ -209,7 +211,8 @@ int attention_layer(float* out, const float* x, const qh_tensor* q_w, const qh_t
   c.prologue = P_LOAD;
   c.x = og;
   c.nseg = 1;
-  c.seg[0] = seg_i8(o_w->w_i8, o_w->scale, kHidden, 0, out, E_STORE);
+  c.rows_per_batch = 4;
+  c.seg[0] = seg_i8(o_w->w_i8, o_w->scale, kHidden, 0, out, E_STORE, 4);
   QH_HIP(launch_gemv(c, 1, s));
   return QH_OK;
 }
@@ -247,7 +250,8 @@ int mlp_layer(float* out, const float* x, const qh_tensor* gate_w, const qh_tens
   c.prologue = P_LOAD;
   c.x = act;
   c.nseg = 1;
-  c.seg[0] = seg_i8(down_w->w_i8, down_w->scale, kHidden, 0, out, E_STORE);
+  c.rows_per_batch = 4;
+  c.seg[0] = seg_i8(down_w->w_i8, down_w->scale, kHidden, 0, out, E_STORE, 4);
   QH_HIP(launch_gemv(c, 1, s));
   return QH_OK;
 }
