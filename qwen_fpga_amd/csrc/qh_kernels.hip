@@ -86,28 +86,41 @@ __device__ __forceinline__ float seg_scale(const Seg& g, int row) {
   return g.sw[row];
 }
 
-// Transposed xor-butterfly over R rows (R = 1, 2, 4, 8): at offsets 32, 16, ...
+// Transposed xor-butterfly over R rows (R = 4 or 8): at offsets 32, 16 (, 8)
 // each lane keeps half of its rows and receives its partner's other half; the
 // remaining offsets finish the tree.  Lane l ends with row (l >> (6 - log2 R))
-// & (R - 1).  Per row this is the 64-lane xor tree of the C16 order.
-template <int R, typename T>
-__device__ __forceinline__ T reduce_rows(T v[R], int lane) {
-  int off = 32;
+// & (R - 1).  Per row this is the 64-lane xor tree of the C16 order.  Written
+// out per R so every index is static (no private array can end up in memory).
+template <typename T>
+__device__ __forceinline__ T reduce4(T v[4], int lane) {
+  {
+    const bool up = (lane & 32) != 0;
 #pragma unroll
-  for (int n = R; n > 1; n >>= 1) {
-    const bool up = (lane & off) != 0;
-#pragma unroll
-    for (int i = 0; i < n / 2; ++i) {
-      const T send = up ? v[i] : v[i + n / 2];
-      const T keep = up ? v[i + n / 2] : v[i];
-      v[i] = keep + __shfl_xor(send, off, 64);
+    for (int i = 0; i < 2; ++i) {
+      const T send = up ? v[i] : v[i + 2];
+      const T keep = up ? v[i + 2] : v[i];
+      v[i] = keep + __shfl_xor(send, 32, 64);
     }
-    off >>= 1;
+  }
+  {
+    const bool up = (lane & 16) != 0;
+    const T send = up ? v[0] : v[1];
+    const T keep = up ? v[1] : v[0];
+    v[0] = keep + __shfl_xor(send, 16, 64);
   }
   T r = v[0];
-#pragma unroll
-  for (int o = 64 / R / 2; o >= 1; o >>= 1) r = r + __shfl_xor(r, o, 64);
+  r = r + __shfl_xor(r, 8, 64);
+  r = r + __shfl_xor(r, 4, 64);
+  r = r + __shfl_xor(r, 2, 64);
+  r = r + __shfl_xor(r, 1, 64);
   return r;
+}
+template <int R, typename T>
+__device__ __forceinline__ T reduce_rows(T v[R], int lane) {
+  if constexpr (R == 8)
+    return reduce8(v, lane);
+  else
+    return reduce4(v, lane);
 }
 template <int R>
 __device__ __forceinline__ int row_of_lane(int lane) {
@@ -118,20 +131,22 @@ __device__ __forceinline__ int row_of_lane(int lane) {
 struct EpiAux {
   float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;   // conv state cols 1..3 | residual | A_log
   float w0 = 0.0f, w1 = 0.0f, w2 = 0.0f, w3 = 0.0f;   // conv taps | dt_bias
+  float sc = 1.0f;                                     // the row's weight scale (int8 segments)
 };
 __device__ __forceinline__ void epi_prefetch(const Seg& g, int myrow, EpiAux& x) {
-  if (myrow >= g.rows) return;
+  const int r = min(myrow, g.rows - 1);   // always a valid address; unused rows are never stored
+  if (g.kind != SEG_F32) x.sc = seg_scale(g, r);
   switch (g.epi) {
     case E_RESID:
-      x.a0 = g.out[myrow];
+      x.a0 = g.out[r];
       break;
     case E_GATE_A:
-      x.a0 = g.c0[myrow];
-      x.w0 = g.c1[myrow];
+      x.a0 = g.c0[r];
+      x.w0 = g.c1[r];
       break;
     case E_CONV: {
-      const float4 st = *reinterpret_cast<const float4*>(g.c2 + (size_t)myrow * 4);
-      const float4 w = *reinterpret_cast<const float4*>(g.c0 + (size_t)myrow * 4);
+      const float4 st = *reinterpret_cast<const float4*>(g.c2 + (size_t)r * 4);
+      const float4 w = *reinterpret_cast<const float4*>(g.c0 + (size_t)r * 4);
       x.a1 = st.y;
       x.a2 = st.z;
       x.a3 = st.w;
@@ -192,33 +207,41 @@ __device__ __forceinline__ void gemv_epilogue(const Seg& g, int lane, int myrow,
   }
 }
 
+// Loads of one batch: every address is clamped into the segment (rows) and the
+// vector (chunks), so the loads are unconditional and issue back to back.  A
+// clamped chunk meets x = 0 (the prologue zeroes chunks beyond K) and a clamped
+// row is never stored, so neither changes a result.
 template <int NCH, int R>
 __device__ __forceinline__ void load_batch(const Seg& g, int row0, int K, int nchunk, int lane,
                                            uint32_t (&w)[NCH][R][4]) {
+  const bool pair = g.kind == SEG_PAIR;
+  const int8_t* w0 = g.w;
+  const int8_t* w1 = pair ? g.w2 : g.w;
+  const int last = g.rows - 1;
 #pragma unroll
-  for (int j = 0; j < NCH; ++j) {
-    const int c = lane + 64 * j;
+  for (int r = 0; r < R; ++r) {
+    const int row = min(row0 + r, last);
+    const int8_t* base = pair ? (((row & 1) ? w1 : w0) + (size_t)(row >> 1) * K) : (w0 + (size_t)row * K);
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      if (c < nchunk && row0 + r < g.rows) {
-        load16b(seg_row(g, row0 + r, K) + 16 * c, w[j][r]);
-      } else {
-        w[j][r][0] = w[j][r][1] = w[j][r][2] = w[j][r][3] = 0u;
-      }
+    for (int j = 0; j < NCH; ++j) {
+      const int c = min(lane + 64 * j, nchunk - 1);
+      load16b(base + 16 * c, w[j][r]);
     }
   }
 }
 
+// Segment of batch b; b is wave-uniform, and readfirstlane makes that visible
+// to the compiler so the descriptor is read with scalar loads.
 __device__ __forceinline__ int seg_of(const GemvArgs& a, int b) {
   int si = 0;
   while (si + 1 < a.nseg && b >= a.seg[si + 1].batch0) ++si;
-  return si;
+  return __builtin_amdgcn_readfirstlane(si);
 }
 
 template <int NCH, int MODE, int PRO, int R>
 __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
-  if (a.done != nullptr && *a.done != 0) return;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwv = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, nwv = blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int K = a.K, nchunk = K >> 4;
   const int total = a.seg[a.nseg - 1].batch0 + a.seg[a.nseg - 1].nbatch;
   const int stride = gridDim.x * nwv;
@@ -235,6 +258,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
     if (g.kind != SEG_F32) load_batch<NCH, R>(g, row0, K, nchunk, lane, w);
     epi_prefetch(g, row0 + row_of_lane<R>(lane), aux);
   }
+  if (a.done != nullptr && *a.done != 0) return;   // engine stop flag (loads above are harmless)
 
   // ---------------- 2. prologue: this lane's chunks c = lane + 64 j of x
   float xv[NCH][16];     // fp32 activation (W8A16) / dequantized q*s (W8A8)
@@ -245,11 +269,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int c = lane + 64 * j;
-      if (c < nchunk) {
-        load16b(a.xq + 16 * c, xq[j]);
-      } else {
-        xq[j][0] = xq[j][1] = xq[j][2] = xq[j][3] = 0u;
-      }
+      load16b(a.xq + 16 * min(c, nchunk - 1), xq[j]);
+      if (c >= nchunk) xq[j][0] = xq[j][1] = xq[j][2] = xq[j][3] = 0u;
 #pragma unroll
       for (int e = 0; e < 16; ++e) xv[j][e] = i8_at(xq[j], e) * xs;
     }
@@ -258,8 +279,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
     if constexpr (PRO == P_NORM || PRO == P_GATED) {
 #pragma unroll
       for (int j = 0; j < NCH; ++j) {
-        const int c = lane + 64 * j;
-        if (c < nchunk) load16f(a.nw + (PRO == P_GATED ? ((16 * c) & 127) : 16 * c), nwv16[j]);
+        const int c = min(lane + 64 * j, nchunk - 1);
+        load16f(a.nw + (PRO == P_GATED ? ((16 * c) & 127) : 16 * c), nwv16[j]);
       }
     }
     if (PRO == P_NORM && a.emb != nullptr) {   // embed_row (gemv.hpp:76-84)
@@ -284,12 +305,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
 #pragma unroll
       for (int j = 0; j < NCH; ++j) {
         const int c = lane + 64 * j;
-        if (c < nchunk) {
-          load16f(a.x + 16 * c, xv[j]);
-        } else {
+        load16f(a.x + 16 * min(c, nchunk - 1), xv[j]);
+        if (c >= nchunk)
 #pragma unroll
           for (int e = 0; e < 16; ++e) xv[j][e] = 0.0f;
-        }
       }
     }
     if constexpr (PRO == P_NORM) {   // norm.hpp:13-20, sum of squares in C16 order
@@ -395,10 +414,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
     }
     if (g.kind == SEG_F32 || MODE == M_W8A16) {
       y = reduce_rows<R>(pf, lane);
-      if (g.kind != SEG_F32 && myrow < g.rows) y = y * seg_scale(g, myrow);
+      if (g.kind != SEG_F32) y = y * aux.sc;
     } else {
       acci = reduce_rows<R>(pi, lane);
-      if (myrow < g.rows) y = ((float)acci * xs) * seg_scale(g, myrow);   // float(acc)*sx*sw
+      y = ((float)acci * xs) * aux.sc;   // float(acc)*sx*sw
     }
     gemv_epilogue<R>(g, lane, myrow, y, acci, aux);
     si = sin;
