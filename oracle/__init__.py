@@ -85,6 +85,15 @@ def lib():
         _sig(L, "or_delta_rule_head", None, [P, P, P, F, F, P, P])
         _sig(L, "or_delta_rule_layer", None, [P, P, P, P, P, P, P])
         _sig(L, "or_quant_act", None, [P, P, P, I])
+        _sig(L, "or_quant_act_markstein", None, [P, P, P, I])
+        _sig(L, "or_dev_gemv_i8", None, [P, P, P, P, I, I])
+        _sig(L, "or_dev_gemv_f32", None, [P, P, P, I, I])
+        _sig(L, "or_dev_rmsnorm", None, [P, P, P, I, F])
+        _sig(L, "or_dev_rmsnorm_gated", None, [P, P, P, P, I, F])
+        _sig(L, "or_dev_l2norm", None, [P, I])
+        _sig(L, "or_dev_conv1d_step", None, [P, P, P, P])
+        _sig(L, "or_dev_delta_rule_head", None, [P, P, P, F, F, P, P])
+        _sig(L, "or_dev_delta_rule_layer", None, [P, P, P, P, P, P, P])
         _sig(L, "or_gemv_w8a8", None, [P, P, P, P, P, F, I, I])
         _sig(L, "or_gemv_acc_i64", None, [P, P, P, I, I])
         _sig(L, "or_deltanet_layer", None, [P, P, T, T, T, T, P, P, P, P, T, P, P, I, I])

@@ -51,10 +51,10 @@ void or_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
 /* ====================================================================
  * Device-order transcendentals.  exp: Cody-Waite reduction by ln2 (two-part
  * constant) and the degree-7 Taylor polynomial of e^r on |r| <= ln2/2, Horner
- * with fma, then exact scaling by 2^n.  log: m*2^e with m in [sqrt(1/2),
- * sqrt(2)), log m = 2 atanh((m-1)/(m+1)) by its odd series to s^11.  log1p:
- * Goldberg's log(1+y)*y/((1+y)-1).  Only IEEE +,-,*,/,fma and bit operations,
- * so the HIP kernels reproduce them bit for bit.
+ * with fma, then exact scaling by 2^n.  log1p: in double, m*2^e with m in
+ * [sqrt(1/2), sqrt(2)), log m = 2 atanh((m-1)/(m+1)) by its odd series to s^21,
+ * rounded once to float.  Only IEEE +,-,*,/,fma and bit operations, so the HIP
+ * kernels reproduce them bit for bit.
  * ================================================================== */
 static inline float f_from_bits(uint32_t b) { float f; memcpy(&f, &b, 4); return f; }
 static inline uint32_t bits_of(float f) { uint32_t b; memcpy(&b, &f, 4); return b; }
@@ -80,30 +80,42 @@ float or_dev_expf(float x) {
   return p * f_from_bits((uint32_t)(ni + 127) << 23);
 }
 
-static float dev_logf_pos(float u) {   /* u finite, >= 1 */
-  const uint32_t b = bits_of(u);
-  int e = (int)((b >> 23) & 0xffu) - 127;
-  float m = f_from_bits((b & 0x007fffffu) | 0x3f800000u);
-  if (m > 1.41421353816986083984375f) { m = m * 0.5f; e += 1; }
-  const float s = (m - 1.0f) / (m + 1.0f);
-  const float s2 = s * s;
-  float t = 9.090909090909091e-2f;
-  t = fmaf(t, s2, 1.111111111111111e-1f);
-  t = fmaf(t, s2, 1.428571428571429e-1f);
-  t = fmaf(t, s2, 2.0e-1f);
-  t = fmaf(t, s2, 3.333333333333333e-1f);
-  t = fmaf(t, s2, 1.0f);
-  const float lm = (2.0f * s) * t;
-  const float fe = (float)e;
-  return fmaf(fe, 0.693145751953125f, fmaf(fe, 1.428606765330187045e-06f, lm));
+/* log(u) for u >= 1 in double: u = m * 2^e with m in [sqrt(1/2), sqrt(2)),
+ * log m = 2 atanh(s), s = (m-1)/(m+1), odd series to s^21 (|s| <= 0.1716),
+ * plus e*ln2 with ln2 split so that e*ln2_hi is exact. */
+static double dev_log_d(double u) {
+  uint64_t b;
+  memcpy(&b, &u, 8);
+  int e = (int)((b >> 52) & 0x7ffu) - 1023;
+  const uint64_t mb = (b & 0x000fffffffffffffull) | 0x3ff0000000000000ull;
+  double m;
+  memcpy(&m, &mb, 8);
+  if (m > 1.4142135623730951) { m = m * 0.5; e += 1; }
+  const double s = (m - 1.0) / (m + 1.0);
+  const double s2 = s * s;
+  double t = 1.0 / 21.0;
+  t = fma(t, s2, 1.0 / 19.0);
+  t = fma(t, s2, 1.0 / 17.0);
+  t = fma(t, s2, 1.0 / 15.0);
+  t = fma(t, s2, 1.0 / 13.0);
+  t = fma(t, s2, 1.0 / 11.0);
+  t = fma(t, s2, 1.0 / 9.0);
+  t = fma(t, s2, 1.0 / 7.0);
+  t = fma(t, s2, 1.0 / 5.0);
+  t = fma(t, s2, 1.0 / 3.0);
+  t = fma(t, s2, 1.0);
+  const double lm = (2.0 * s) * t;
+  const double fe = (double)e;
+  return fma(fe, 6.93147180369123816490e-01, fma(fe, 1.90821492927058770002e-10, lm));
 }
 
-float or_dev_log1pf(float y) {   /* y >= 0 (softplus argument range) */
+/* log1p for y >= 0: y itself below 2^-28 (where y is the rounded log1p), else
+ * the double log of 1 + y (exact in double there), rounded once to float. */
+float or_dev_log1pf(float y) {
   if (y != y) return y;
   if (y == INFINITY) return y;
-  if (y < 1e-4f) return fmaf(-0.5f * y, y, y);
-  const float u = 1.0f + y;
-  return dev_logf_pos(u) * (y / (u - 1.0f));
+  if (y < 3.7252902984619140625e-09f) return y;
+  return (float)dev_log_d(1.0 + (double)y);
 }
 
 /* ---- activations.hpp:7-14 ---- */
@@ -348,7 +360,56 @@ void or_delta_rule_layer(const float* q, const float* k, const float* v, const f
                        out + h * LV);
 }
 
+/* ---- device-order primitives (the twin of each gfx950 op kernel) ---- */
+void or_dev_gemv_i8(float* y, const int8_t* w, const float* scale, const float* x, int out, int in) {
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+  for (int o = 0; o < out; ++o) y[o] = c16_dot_i8(w + (long)o * in, x, in) * scale[o];
+}
+void or_dev_gemv_f32(float* y, const float* w, const float* x, int out, int in) {
+  for (int o = 0; o < out; ++o) y[o] = c16_dot_f32(w + (long)o * in, x, in);
+}
+void or_dev_rmsnorm(float* y, const float* x, const float* w, int n, float eps) {
+  rmsnorm_o(y, x, w, n, eps, OR_ORDER_DEV);
+}
+void or_dev_rmsnorm_gated(float* y, const float* x, const float* w, const float* z, int n, float eps) {
+  rmsnorm_gated_o(y, x, w, z, n, eps, OR_ORDER_DEV);
+}
+void or_dev_l2norm(float* v, int n) { l2norm_o(v, n, OR_ORDER_DEV); }
+void or_dev_conv1d_step(float* out, const float* in_ch, float* state, const float* weight) {
+  conv1d_step_o(out, in_ch, state, weight, OR_ORDER_DEV);
+}
+void or_dev_delta_rule_head(const float* q, const float* k, const float* v, float g, float beta, float* S,
+                            float* out) {
+  delta_rule_head_dev(q, k, v, g, beta, S, out);
+}
+void or_dev_delta_rule_layer(const float* q, const float* k, const float* v, const float* g,
+                             const float* beta, float* S, float* out) {
+  for (int h = 0; h < LH; ++h)
+    delta_rule_head_dev(q + h * LK, k + h * LK, v + h * LV, g[h], beta[h], S + (long)h * LK * LV, out + h * LV);
+}
+
 /* ---- W8A8 ---- */
+/* The gfx950 quantizer forms x/s as Markstein's correction from rs = RN(1/s)
+ * (q0 = x*rs, r = fma(-s, q0, x), q = fma(r, rs, q0)); restated here so a test
+ * can compare it with the true division of or_quant_act. */
+void or_quant_act_markstein(int8_t* q, float* s, const float* x, int n) {
+  float amax = 0.0f;
+  for (int i = 0; i < n; ++i) {
+    const float a = fabsf(x[i]);
+    if (a > amax) amax = a;
+  }
+  const float sc = amax > 0.0f ? amax / 127.0f : 1.0f;
+  const float rs = 1.0f / sc;
+  for (int i = 0; i < n; ++i) {
+    const float q0 = x[i] * rs;
+    const float r = fmaf(-sc, q0, x[i]);
+    float t = rintf(fmaf(r, rs, q0));
+    t = fminf(fmaxf(t, -127.0f), 127.0f);
+    q[i] = (int8_t)t;
+  }
+  *s = sc;
+}
+
 void or_quant_act(int8_t* q, float* s, const float* x, int n) {
   float amax = 0.0f;   /* model.py:41-45; export_gemv_tv.py:25-30 */
   for (int i = 0; i < n; ++i) {
@@ -358,8 +419,7 @@ void or_quant_act(int8_t* q, float* s, const float* x, int n) {
   const float sc = amax > 0.0f ? amax / 127.0f : 1.0f;
   for (int i = 0; i < n; ++i) {
     float r = rintf(x[i] / sc);
-    if (r > 127.0f) r = 127.0f;
-    if (r < -127.0f) r = -127.0f;
+    r = fminf(fmaxf(r, -127.0f), 127.0f);   /* clip(-127, 127); NaN maps to -127 */
     q[i] = (int8_t)r;
   }
   *s = sc;

@@ -68,6 +68,20 @@ void or_delta_rule_head(const float* q, const float* k, const float* v, float g,
 void or_delta_rule_layer(const float* q, const float* k, const float* v, const float* g,
                          const float* beta, float* S, float* out);
 
+/* ---- device-order primitives: the bit-exact twins of the gfx950 op kernels ---- */
+void or_dev_gemv_i8(float* y, const int8_t* w, const float* scale, const float* x, int out, int in);
+void or_dev_gemv_f32(float* y, const float* w, const float* x, int out, int in);
+void or_dev_rmsnorm(float* y, const float* x, const float* w, int n, float eps);
+void or_dev_rmsnorm_gated(float* y, const float* x, const float* w, const float* z, int n, float eps);
+void or_dev_l2norm(float* v, int n);
+void or_dev_conv1d_step(float* out, const float* in_ch, float* state, const float* weight);
+void or_dev_delta_rule_head(const float* q, const float* k, const float* v, float g, float beta, float* S,
+                            float* out);
+void or_dev_delta_rule_layer(const float* q, const float* k, const float* v, const float* g,
+                             const float* beta, float* S, float* out);
+/* act-quant with the device's reciprocal-corrected quotient (must equal or_quant_act) */
+void or_quant_act_markstein(int8_t* q, float* s, const float* x, int n);
+
 /* ---- W8A8 primitives ---- */
 /* model.py:37-45 _qa / export_gemv_tv.py:25-30 q_i8_vec */
 void or_quant_act(int8_t* q, float* s, const float* x, int n);

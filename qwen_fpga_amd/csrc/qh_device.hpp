@@ -44,33 +44,39 @@ __device__ __forceinline__ float dev_expf(float x) {
   return p * __uint_as_float((uint32_t)(ni + 127) << 23);
 }
 
-// log for u >= 1: u = m*2^e, m in [sqrt(1/2), sqrt(2)); log m = 2*atanh(s),
-// s = (m-1)/(m+1), odd series to s^11; e*ln2 added with the two-part ln2.
-__device__ __forceinline__ float dev_logf_ge1(float u) {
-  const uint32_t b = __float_as_uint(u);
-  int e = (int)((b >> 23) & 0xffu) - 127;
-  float m = __uint_as_float((b & 0x007fffffu) | 0x3f800000u);
-  if (m > 1.41421353816986083984375f) { m = m * 0.5f; e += 1; }
-  const float s = (m - 1.0f) / (m + 1.0f);
-  const float s2 = s * s;
-  float t = 9.090909090909091e-2f;
-  t = __builtin_fmaf(t, s2, 1.111111111111111e-1f);
-  t = __builtin_fmaf(t, s2, 1.428571428571429e-1f);
-  t = __builtin_fmaf(t, s2, 2.0e-1f);
-  t = __builtin_fmaf(t, s2, 3.333333333333333e-1f);
-  t = __builtin_fmaf(t, s2, 1.0f);
-  const float lm = (2.0f * s) * t;
-  const float fe = (float)e;
-  return __builtin_fmaf(fe, 0.693145751953125f, __builtin_fmaf(fe, 1.428606765330187045e-06f, lm));
+// log(u) for u >= 1 in double: u = m*2^e, m in [sqrt(1/2), sqrt(2)); log m =
+// 2*atanh(s), s = (m-1)/(m+1), odd series to s^21; e*ln2 with ln2 split so that
+// e*ln2_hi is exact.
+__device__ __forceinline__ double dev_log_d(double u) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(u);
+  int e = (int)((b >> 52) & 0x7ffu) - 1023;
+  double m = __longlong_as_double((long long)((b & 0x000fffffffffffffull) | 0x3ff0000000000000ull));
+  if (m > 1.4142135623730951) { m = m * 0.5; e += 1; }
+  const double s = (m - 1.0) / (m + 1.0);
+  const double s2 = s * s;
+  double t = 1.0 / 21.0;
+  t = __builtin_fma(t, s2, 1.0 / 19.0);
+  t = __builtin_fma(t, s2, 1.0 / 17.0);
+  t = __builtin_fma(t, s2, 1.0 / 15.0);
+  t = __builtin_fma(t, s2, 1.0 / 13.0);
+  t = __builtin_fma(t, s2, 1.0 / 11.0);
+  t = __builtin_fma(t, s2, 1.0 / 9.0);
+  t = __builtin_fma(t, s2, 1.0 / 7.0);
+  t = __builtin_fma(t, s2, 1.0 / 5.0);
+  t = __builtin_fma(t, s2, 1.0 / 3.0);
+  t = __builtin_fma(t, s2, 1.0);
+  const double lm = (2.0 * s) * t;
+  const double fe = (double)e;
+  return __builtin_fma(fe, 6.93147180369123816490e-01, __builtin_fma(fe, 1.90821492927058770002e-10, lm));
 }
 
-// log1p for y >= 0 (Goldberg: log(1+y) * y / ((1+y) - 1)).
+// log1p for y >= 0: y itself below 2^-28 (the rounded log1p there), else the
+// double log of 1 + y (exact in double), rounded once to float.
 __device__ __forceinline__ float dev_log1pf(float y) {
   if (y != y) return y;
   if (y == __builtin_inff()) return y;
-  if (y < 1e-4f) return __builtin_fmaf(-0.5f * y, y, y);
-  const float u = 1.0f + y;
-  return dev_logf_ge1(u) * (y / (u - 1.0f));
+  if (y < 3.7252902984619140625e-09f) return y;
+  return (float)dev_log_d(1.0 + (double)y);
 }
 
 // hls/src/activations.hpp:7-14 with the device exp / log1p.
