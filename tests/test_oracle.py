@@ -488,3 +488,25 @@ def test_device_order_close_to_reference(orc, blob, idx):
     for layer in range(18):   # reassociation drift grows with depth; normalised per layer
         err = np.abs(a[layer] - b[layer]).max() / np.abs(b[layer]).max()
         assert err < 1e-4, (layer, err)
+
+
+def test_golden_decode_fixture(orc, blob, idx):
+    """tests/golden/decode_ref_c5.json came from the compiled reference qwen_top; the
+    reference-order restatement reproduces its first 64 steps (argmax, and the step-0 and
+    step-63 logits to the bit via their sha256)."""
+    import hashlib
+    import json
+    import os
+
+    from conftest import GOLDEN
+    g = json.load(open(os.path.join(GOLDEN, "decode_ref_c5.json")))
+    assert g["blob_sha256"] == hashlib.sha256(blob.tobytes()).hexdigest()
+    assert len(g["fed"]) == g["n_prompt"] + g["n_new"] == 576
+    assert g["fed"][g["n_prompt"]:] == g["argmax"][g["n_prompt"] - 1:-1]   # the run_hls feedback
+    m = orc.Model(blob, idx, 64)
+    for i in range(64):
+        want = str(i) in g["logits"]
+        a, lg = m.decode_token(g["fed"][i], orc.W8A16, orc.ORDER_REF, want_logits=want)
+        assert a == g["argmax"][i], i
+        if want:
+            assert hashlib.sha256(lg.astype("<f4").tobytes()).hexdigest() == g["logits"][str(i)]["sha256"], i
