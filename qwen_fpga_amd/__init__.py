@@ -83,6 +83,15 @@ def _lib() -> ctypes.CDLL:
     if _LIB is None:
         if not os.path.exists(LIB_PATH):
             raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() first")
+        # One HIP runtime per process.  torch ships its own libamdhip64 (and HSA
+        # runtime) under the same soname that libqh.so needs: loaded first, it
+        # satisfies libqh's dependency.  Loaded after libqh, it maps a second
+        # runtime beside /opt/rocm's, and the one initialised second sees no
+        # device.  So when torch is importable it is loaded before libqh.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         lib = ctypes.CDLL(LIB_PATH)
         lib.qh_strerror.restype = ctypes.c_char_p
         lib.qh_blob_size.restype = ctypes.c_size_t

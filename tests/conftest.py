@@ -89,3 +89,15 @@ def assert_close(got, exp, rtol=1e-4, atol=1e-5, what=""):
         i = int(np.flatnonzero(bad)[0])
         raise AssertionError(f"{what}: {int(bad.sum())} of {g.size} outside rtol={rtol} atol={atol}; "
                              f"first at {i}: {g.flat[i]!r} vs {e.flat[i]!r}; max|d|={err.max():.3e}")
+
+
+def assert_close_norm(got, exp, rel, what=""):
+    """max |got - exp| <= rel * max |exp|: the reassociation bound for a vector whose
+    elements come from long fp32 sums (immune to cancellation in single elements)."""
+    g, e = np.asarray(got, dtype=np.float64), np.asarray(exp, dtype=np.float64)
+    err = np.abs(g - e).max()
+    scale = np.abs(e).max()
+    if err > rel * scale:
+        i = int(np.argmax(np.abs(g - e)))
+        raise AssertionError(f"{what}: max|d|={err:.3e} > {rel:g} * max|exp|={scale:.3e}; at {i}: "
+                             f"{g.flat[i]!r} vs {e.flat[i]!r}")

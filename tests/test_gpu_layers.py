@@ -4,7 +4,7 @@ context (C3) against the device twin and float64, and the 4-layer block (C4)."""
 import numpy as np
 import pytest
 
-from conftest import assert_bitwise, assert_close, rng
+from conftest import assert_bitwise, assert_close_norm, rng
 
 pytestmark = pytest.mark.gpu
 
@@ -91,8 +91,8 @@ def test_deltanet_layer(q, orc, W, w8a8):
     if not w8a8:
         o2, r2, c2 = np.empty(1024, np.float32), rec0.copy(), conv0.copy()
         orc.lib().or_deltanet_layer(*args(o2, r2, c2), mode, orc.ORDER_REF)
-        assert_close(out_d.cpu().numpy(), o2, rtol=1e-4, atol=1e-4, what="out vs reference order")
-        assert_close(rec_d.cpu().numpy(), r2, rtol=0, atol=2e-5, what="rec vs reference order")
+        assert_close_norm(out_d.cpu().numpy(), o2, 1e-4, what="out vs reference order")
+        assert_close_norm(rec_d.cpu().numpy(), r2, 1e-4, what="rec vs reference order")
 
 
 def _attn_args(q, W, pre):
@@ -129,7 +129,7 @@ def test_attention_layer(q, orc, W, w8a8, Tpast):
                                      W.ot[pre + "v_proj.weight"], W.ot[pre + "o_proj.weight"],
                                      p(W.host(pre + "q_norm.weight")[0]), p(W.host(pre + "k_norm.weight")[0]),
                                      Tpast, p(k2), p(v2), Tpast, mode, orc.ORDER_REF)
-        assert_close(out_d.cpu().numpy(), o2, rtol=1e-4, atol=1e-4, what="attention vs reference order")
+        assert_close_norm(out_d.cpu().numpy(), o2, 1e-4, what="attention vs reference order")
 
 
 @pytest.mark.parametrize("T", [511, 4095, 32767])
@@ -171,7 +171,7 @@ def test_mlp_layer(q, orc, W, w8a8):
         o2 = np.empty(1024, np.float32)
         orc.lib().or_mlp_layer(p(o2), p(x), W.ot[pre + "gate_proj.weight"], W.ot[pre + "up_proj.weight"],
                                W.ot[pre + "down_proj.weight"], mode, orc.ORDER_REF)
-        assert_close(out_d.cpu().numpy(), o2, rtol=1e-4, atol=1e-3, what="mlp vs reference order")
+        assert_close_norm(out_d.cpu().numpy(), o2, 1e-4, what="mlp vs reference order")
 
 
 def test_deltanet_64_steps(q, orc, W):

@@ -12,7 +12,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from conftest import assert_bitwise, assert_close, rng
+from conftest import assert_bitwise, assert_close, assert_close_norm, rng
 
 pytestmark = pytest.mark.gpu
 
@@ -61,7 +61,7 @@ def test_gemv_i8_w8a16(q, orc, T, out, inn):
     orc.lib().or_dev_gemv_i8(p(dev), p(w), p(s), p(x), out, inn)
     orc.lib().or_gemv_i8(p(ref), p(w), p(s), p(x), out, inn)
     assert_bitwise(got, dev, "gemv_i8 vs device twin")
-    assert_close(got, ref, rtol=1e-4, atol=1e-5, what="gemv_i8 vs reference order")
+    assert_close_norm(got, ref, 1e-5, what="gemv_i8 vs reference order")
 
 
 @pytest.mark.parametrize("out,inn", [(3584, 1024), (1024, 3584), (6144, 1024)])
@@ -116,7 +116,7 @@ def test_small_ops(q, orc, T):
     L.or_dev_gemv_f32(p(dev), p(w), p(x), 16, 1024)
     L.or_gemv_f32(p(ref), p(w), p(x), 16, 1024)
     assert_bitwise(T.down(y), dev, "gemv_f32")
-    assert_close(T.down(y), ref, what="gemv_f32 vs ref")
+    assert_close_norm(T.down(y), ref, 1e-5, what="gemv_f32 vs ref")
     E = r.integers(-127, 128, size=(300, 1024)).astype(np.int8)
     es = f32(r.uniform(1e-3, 1e-2, 300))
     Ed, esd, xd = T.up(E), T.up(es), T.up(x)
@@ -167,7 +167,7 @@ def test_conv_and_rope(q, orc, T):
     assert_bitwise(T.down(st_d), so, "conv state")
     sr, orr = st.copy(), np.empty(6144, np.float32)
     L.or_conv1d_step(p(orr), p(inp), p(sr), p(w))
-    assert_close(T.down(out_d), orr, rtol=1e-6, atol=1e-7, what="conv vs ref")
+    assert_close_norm(T.down(out_d), orr, 1e-6, what="conv vs ref")
     for pos in (0, 1, 575, 32767):
         c_d, s_d = T.empty(64), T.empty(64)
         q.rope_cos_sin(pos, c_d, s_d)
