@@ -42,6 +42,7 @@ extern "C" {
 #define QH_EFORMAT (-4)  /* weight index or blob does not match the layout  */
 #define QH_ENOMEM (-5)   /* host or device allocation failed                */
 #define QH_ESTATE (-6)   /* engine not in a state that allows the call      */
+#define QH_EDEVICE (-7)  /* a device-side wait timed out (grid barrier)      */
 
 /* ---- model dimensions (hls/src/types.hpp:20-44) ----------------------- */
 #define QH_HIDDEN 1024
@@ -188,6 +189,18 @@ int qh_engine_create_from_memory(const void* blob, size_t blob_len, const char* 
 int qh_engine_destroy(qh_engine* e);
 /* QH_MODE_W8A16 (default) or QH_MODE_W8A8. */
 int qh_engine_set_mode(qh_engine* e, int mode);
+/* How decode_token / generate run a token; both are bit-identical.
+ * QH_EXEC_PERSISTENT: one cooperative launch per call runs every token, stage
+ * after stage, with grid barriers in between.  QH_EXEC_GRAPH (default): one
+ * replayed hipGraph of per-stage kernels per token.  No counterpart in the reference (its top is one HLS
+ * function); returns QH_ESTATE if the device cannot run the persistent kernel.
+ * If a cooperative launch is refused at run time (another process can hold the
+ * device's cooperative-launch resources), the engine switches itself to
+ * QH_EXEC_GRAPH and completes the call there; qh_engine_get_exec reports it. */
+#define QH_EXEC_PERSISTENT 0
+#define QH_EXEC_GRAPH 1
+int qh_engine_set_exec(qh_engine* e, int exec);
+int qh_engine_get_exec(const qh_engine* e);
 /* Zero recurrent/conv state, empty KV cache, pos = 0 (state.hpp:24-34). */
 int qh_engine_reset(qh_engine* e);
 /* Decode one token (qwen_top): returns the argmax (ties -> lowest id) in
@@ -197,7 +210,8 @@ int qh_decode_token(qh_engine* e, int tok, float* logits, int* argmax_out);
 /* The run_hls loop (run_hls.cpp:56-66) on the device: feed n_prompt ids, then
  * greedily generate up to n_new ids, stopping before emitting `eos` (eos < 0:
  * never).  out_ids receives the generated ids, *n_out their count.  The token
- * feedback stays on the device; the host only launches step graphs. */
+ * feedback stays on the device: one persistent launch (or one graph replay per
+ * token) and no host round trip between tokens. */
 int qh_generate(qh_engine* e, const int* prompt, int n_prompt, int n_new, int eos, int* out_ids,
                 int* n_out);
 /* Tokens processed so far (DecodeState::pos). */

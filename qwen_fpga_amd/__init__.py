@@ -38,7 +38,8 @@ NH, NKV, HD, Q_PROJ, KV_PROJ, ROPE_DIM = 8, 2, 256, 4096, 512, 64
 EPS = 1e-6
 MODE_W8A16, MODE_W8A8 = 0, 1
 
-QH_OK, QH_EINVAL, QH_ERANGE, QH_EIO, QH_EFORMAT, QH_ENOMEM, QH_ESTATE = 0, -1, -2, -3, -4, -5, -6
+QH_OK, QH_EINVAL, QH_ERANGE, QH_EIO, QH_EFORMAT, QH_ENOMEM, QH_ESTATE, QH_EDEVICE = 0, -1, -2, -3, -4, -5, -6, -7
+EXEC_PERSISTENT, EXEC_GRAPH = 0, 1
 
 
 class QHError(RuntimeError):
@@ -360,6 +361,14 @@ class Engine:
 
     def reset(self):
         _check(_lib().qh_engine_reset(self._h), "qh_engine_reset")
+
+    def set_exec(self, exec_kind: int):
+        """EXEC_PERSISTENT (one cooperative launch per call) or EXEC_GRAPH (a graph per token)."""
+        _check(_lib().qh_engine_set_exec(self._h, ctypes.c_int(exec_kind)), "qh_engine_set_exec")
+
+    @property
+    def exec_kind(self) -> int:
+        return int(_lib().qh_engine_get_exec(self._h))
 
     @property
     def pos(self) -> int:

@@ -10,12 +10,15 @@ namespace qh {
 // hipError_t -> status (0 ok, positive hipError_t otherwise)
 inline int hip_status(hipError_t e) { return e == hipSuccess ? QH_OK : (int)e; }
 
+// With QH_VERBOSE=1 in the environment, a failing HIP call is named on stderr.
+int hip_report(hipError_t e, const char* what, const char* file, int line);
+
 #define QH_TRY(expr)                         \
   do {                                       \
     const int st_ = (expr);                  \
     if (st_ != QH_OK) return st_;            \
   } while (0)
-#define QH_HIP(expr) QH_TRY(::qh::hip_status(expr))
+#define QH_HIP(expr) QH_TRY(::qh::hip_report((expr), #expr, __FILE__, __LINE__))
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 

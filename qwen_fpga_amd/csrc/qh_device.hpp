@@ -159,4 +159,63 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
          ((uint32_t)(d & 0xff) << 24);
 }
 
+// Device-coherent access to the activation vectors that workgroups hand to one
+// another: loads and stores with the sc1 cache-policy bit (device scope), which
+// bypass the per-XCD L2 state.  Within one kernel launch a workgroup on
+// another XCD sees such a store once it has completed; an ordinary load could
+// hit a stale line in its own XCD's L2.  The vector forms are plain buffer
+// loads/stores (not atomics), so a lane's loads issue back to back; their base
+// pointer must be the same on every lane of the wave.  Weights and state that
+// one workgroup owns use ordinary accesses.
+constexpr int kSc1 = 16;   // cache-policy operand: sc1
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coh_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7ffffff0, 0x00020000);
+}
+__device__ __forceinline__ float ldc(const float* p) {
+  return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ int ldc_i(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void stc(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void stc_i(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// base[idx] (uniform base, per-lane idx)
+__device__ __forceinline__ float ldcb(const float* base, int idx) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(coh_rsrc(base), idx * 4, 0, kSc1));
+}
+__device__ __forceinline__ void stcb(float* base, int idx, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), coh_rsrc(base), idx * 4, 0, kSc1);
+}
+// base[idx .. idx+3], idx a multiple of 4
+__device__ __forceinline__ void ldc4(const float* base, int idx, float* v) {
+  const auto u = __builtin_amdgcn_raw_buffer_load_b128(coh_rsrc(base), idx * 4, 0, kSc1);
+  v[0] = __uint_as_float(u[0]);
+  v[1] = __uint_as_float(u[1]);
+  v[2] = __uint_as_float(u[2]);
+  v[3] = __uint_as_float(u[3]);
+}
+__device__ __forceinline__ void stc4(float* base, int idx, const float* v) {
+  __attribute__((ext_vector_type(4))) uint32_t u;
+  u[0] = __float_as_uint(v[0]);
+  u[1] = __float_as_uint(v[1]);
+  u[2] = __float_as_uint(v[2]);
+  u[3] = __float_as_uint(v[3]);
+  __builtin_amdgcn_raw_buffer_store_b128(u, coh_rsrc(base), idx * 4, 0, kSc1);
+}
+// base[idx .. idx+15], idx a multiple of 4
+__device__ __forceinline__ void ldc16(const float* base, int idx, float* v) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) ldc4(base, idx + 4 * k, v + 4 * k);
+}
+__device__ __forceinline__ void stc16(float* base, int idx, const float* v) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) stc4(base, idx + 4 * k, v + 4 * k);
+}
+
 }  // namespace qh

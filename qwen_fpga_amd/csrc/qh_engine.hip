@@ -9,6 +9,7 @@
 #include <unistd.h>
 
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <fstream>
 #include <sstream>
@@ -60,6 +61,12 @@ struct qh_engine {
   int last_argmax = -1;
   // graphs[mode][logits][advance]
   hipGraphExec_t graphs[2][2][2] = {};
+  // persistent path: the per-token stage program per mode, barrier counters
+  int exec = QH_EXEC_GRAPH;
+  int persist_grid = 0;          // 0: cooperative launch not available (graph path only)
+  Stage* prog[2] = {};
+  int prog_n = 0;
+  unsigned* bar = nullptr;       // kBarCounters * kBarStride counters + abort flag
 };
 
 namespace {
@@ -86,9 +93,23 @@ Seg mkseg(int kind, int epi, int rows, int batch0, float* out, int rpb = kRowsPe
   return g;
 }
 
-// Enqueue layers [l0, l1) of one decode step on the residual stream e->h.
-int enqueue_layers(qh_engine* e, int l0, int l1, bool embed, hipStream_t s) {
-  const int* done = &e->ctl->done;
+template <class T>
+int dalloc(T** p, size_t n) {
+  return hip_status(hipMalloc(reinterpret_cast<void**>(p), n * sizeof(T)));
+}
+
+Stage gemv_stage(int kind, const GemvArgs& a) {
+  Stage st;
+  st.kind = kind;
+  st.g = a;
+  return st;
+}
+
+// The stages of layers [l0, l1) of one decode step on the residual stream
+// e->h.  `persistent` leaves the device StepCtl pointers out: the persistent
+// kernel passes the token and position itself and stops at its own barrier.
+void build_layers(const qh_engine* e, int l0, int l1, bool embed, bool persistent, std::vector<Stage>& out) {
+  const int* done = persistent ? nullptr : &e->ctl->done;
   int li = 0, fi = 0;
   for (int l = 0; l < l0; ++l) (is_linear(l) ? li : fi)++;
   for (int l = l0; l < l1; ++l) {
@@ -105,10 +126,10 @@ int enqueue_layers(qh_engine* e, int l0, int l1, bool embed, hipStream_t s) {
       if (embed && l == l0) {   // embed_row (qwen_synth.hpp:42-43), written to the residual
         a.emb = i8p(e, kLayers, R_EMBED);
         a.emb_s = scp(e, kLayers, R_EMBED);
-        a.tok = &e->ctl->tok;
+        a.tok = persistent ? nullptr : &e->ctl->tok;
         a.h_out = e->h;
       }
-      a.nseg = 4;
+      a.nseg = 2;   // the fp32 gate projections b, a run in the DeltaNet stage
       a.seg[0] = mkseg(SEG_I8, E_CONV, kConvDim, 0, e->convd);
       a.seg[0].w = i8p(e, l, R_QKV);
       a.seg[0].sw = scp(e, l, R_QKV);
@@ -117,20 +138,30 @@ int enqueue_layers(qh_engine* e, int l0, int l1, bool embed, hipStream_t s) {
       a.seg[1] = mkseg(SEG_I8, E_SILU, kZDim, a.seg[0].nbatch, e->zb);   // silu(z) for the gated norm
       a.seg[1].w = i8p(e, l, R_Z);
       a.seg[1].sw = scp(e, l, R_Z);
-      a.seg[2] = mkseg(SEG_F32, E_GATE_B, kLH, a.seg[1].batch0 + a.seg[1].nbatch, e->gb + 16);
-      a.seg[2].wf = f32p(e, l, R_B);
-      a.seg[3] = mkseg(SEG_F32, E_GATE_A, kLH, a.seg[2].batch0 + a.seg[2].nbatch, e->gb);
-      a.seg[3].wf = f32p(e, l, R_A);
-      a.seg[3].c0 = f32p(e, l, R_ALOG);
-      a.seg[3].c1 = f32p(e, l, R_DTB);
-      QH_HIP(launch_gemv(a, 4, s));
-      DnArgs d;   // l2norm, delta rule (deltanet.hpp:166-173)
+      out.push_back(gemv_stage(ST_GEMV_NORM_1x8, a));
+      DnArgs d;   // gates b, a (deltanet.hpp:164-165), l2norm, delta rule (deltanet.hpp:166-173)
       d.convd = e->convd;
       d.gb = e->gb;
+      d.gx = e->h;
+      d.gx_norm = f32p(e, l, R_IN_LN);
+      d.eps = kEps;
+      d.wb = f32p(e, l, R_B);
+      d.wa = f32p(e, l, R_A);
+      d.A_log = f32p(e, l, R_ALOG);
+      d.dt_bias = f32p(e, l, R_DTB);
+      d.mode = e->mode;
+      if (embed && l == l0) {   // layer 0 reads the embedded token, not the residual
+        d.emb = i8p(e, kLayers, R_EMBED);
+        d.emb_s = scp(e, kLayers, R_EMBED);
+        d.tok = persistent ? nullptr : &e->ctl->tok;
+      }
       d.S = e->rec + (size_t)li * kLH * kLK * kLV;
       d.o = e->o;
       d.done = done;
-      QH_HIP(launch_deltanet(d, s));
+      Stage sd;
+      sd.kind = ST_DELTANET;
+      sd.d = d;
+      out.push_back(sd);
       GemvArgs c;   // gated rmsnorm (+ quant) -> out_proj, residual add (deltanet.hpp:177-181)
       c.K = kLH * kLV;
       c.mode = e->mode;
@@ -145,7 +176,7 @@ int enqueue_layers(qh_engine* e, int l0, int l1, bool embed, hipStream_t s) {
       c.seg[0] = mkseg(SEG_I8, E_RESID, kHidden, 0, e->h, 4);
       c.seg[0].w = i8p(e, l, R_OUTP);
       c.seg[0].sw = scp(e, l, R_OUTP);
-      QH_HIP(launch_gemv(c, 1, s));
+      out.push_back(gemv_stage(ST_GEMV_GATED_2x4, c));
       ++li;
     } else {
       GemvArgs a;   // in_ln rmsnorm (+ quant) -> q||gate, k, v (attention.hpp:31-33)
@@ -166,7 +197,7 @@ int enqueue_layers(qh_engine* e, int l0, int l1, bool embed, hipStream_t s) {
       a.seg[2] = mkseg(SEG_I8, E_STORE, kKVProj, a.seg[1].batch0 + a.seg[1].nbatch, e->vraw);
       a.seg[2].w = i8p(e, l, R_VP);
       a.seg[2].sw = scp(e, l, R_VP);
-      QH_HIP(launch_gemv(a, 4, s));
+      out.push_back(gemv_stage(ST_GEMV_NORM_1x8, a));
       AttnArgs at;
       at.qg = e->qg;
       at.kraw = e->kraw;
@@ -176,8 +207,8 @@ int enqueue_layers(qh_engine* e, int l0, int l1, bool embed, hipStream_t s) {
       at.rope = e->rope;
       at.kc = e->kc + (size_t)fi * e->max_ctx * kKVProj;
       at.vc = e->vc + (size_t)fi * e->max_ctx * kKVProj;
-      at.T = &e->ctl->pos;
-      at.rope_row = &e->ctl->pos;
+      at.T = persistent ? nullptr : &e->ctl->pos;
+      at.rope_row = persistent ? nullptr : &e->ctl->pos;
       at.pm = e->pm;
       at.pl = e->pl;
       at.pacc = e->pacc;
@@ -186,8 +217,12 @@ int enqueue_layers(qh_engine* e, int l0, int l1, bool embed, hipStream_t s) {
       at.og = e->og;
       at.eps = kEps;
       at.done = done;
-      QH_HIP(launch_attn(at, s));
-      QH_HIP(launch_attn_combine(at, s));
+      Stage sa;
+      sa.kind = ST_ATTN;
+      sa.at = at;
+      out.push_back(sa);
+      sa.kind = ST_COMBINE;
+      out.push_back(sa);
       GemvArgs c;   // (+ quant) o_proj, residual add (attention.hpp:94)
       c.K = kNH * kHD;
       c.mode = e->mode;
@@ -199,7 +234,7 @@ int enqueue_layers(qh_engine* e, int l0, int l1, bool embed, hipStream_t s) {
       c.seg[0] = mkseg(SEG_I8, E_RESID, kHidden, 0, e->h, 4);
       c.seg[0].w = i8p(e, l, R_OP);
       c.seg[0].sw = scp(e, l, R_OP);
-      QH_HIP(launch_gemv(c, 1, s));
+      out.push_back(gemv_stage(ST_GEMV_LOAD_2x4, c));
       ++fi;
     }
     // post_ln rmsnorm (+ quant) -> gate||up pairs with SwiGLU -> down, residual (mlp.hpp:11-19)
@@ -217,7 +252,7 @@ int enqueue_layers(qh_engine* e, int l0, int l1, bool embed, hipStream_t s) {
     m.seg[0].sw = scp(e, l, R_GATE);
     m.seg[0].w2 = i8p(e, l, R_UP);
     m.seg[0].sw2 = scp(e, l, R_UP);
-    QH_HIP(launch_gemv(m, 4, s));
+    out.push_back(gemv_stage(ST_GEMV_NORM_1x8, m));
     GemvArgs dn;
     dn.K = kInter;
     dn.mode = e->mode;
@@ -229,17 +264,15 @@ int enqueue_layers(qh_engine* e, int l0, int l1, bool embed, hipStream_t s) {
     dn.seg[0] = mkseg(SEG_I8, E_RESID, kHidden, 0, e->h, 4);
     dn.seg[0].w = i8p(e, l, R_DOWN);
     dn.seg[0].sw = scp(e, l, R_DOWN);
-    QH_HIP(launch_gemv(dn, 1, s));
+    out.push_back(gemv_stage(ST_GEMV_LOAD_4x4, dn));
   }
-  return QH_OK;
 }
 
-// One full decode step (qwen_top): embed, 24 layers, final norm, tied head,
-// argmax (+ pos), optionally the generation bookkeeping.
-int enqueue_step(qh_engine* e, bool with_logits, bool advance, hipStream_t s,
-                 hipEvent_t head_t0 = nullptr, hipEvent_t head_t1 = nullptr) {
-  QH_TRY(enqueue_layers(e, 0, kLayers, true, s));
-  HeadArgs hd;
+// Final norm + tied LM head (qwen_synth.hpp:74-88).
+Stage head_stage(const qh_engine* e, bool with_logits) {
+  Stage st;
+  st.kind = ST_HEAD;
+  HeadArgs& hd = st.hd;
   hd.h = e->h;
   hd.nw = f32p(e, kLayers, R_FINAL);
   hd.eps = kEps;
@@ -250,10 +283,134 @@ int enqueue_step(qh_engine* e, bool with_logits, bool advance, hipStream_t s,
   hd.part_val = e->part_val;
   hd.part_idx = e->part_idx;
   hd.done = &e->ctl->done;
-  if (head_t0) QH_HIP(hipEventRecord(head_t0, s));
-  QH_HIP(launch_head(hd, e->head_grid, s));
-  if (head_t1) QH_HIP(hipEventRecord(head_t1, s));
-  QH_HIP(launch_argmax(e->part_val, e->part_idx, e->head_grid, e->ctl, nullptr, s));
+  return st;
+}
+
+// Stream launches of a stage list (the per-stage kernels); the head is followed
+// by the cross-block argmax, which also advances pos.
+int launch_stages(qh_engine* e, const std::vector<Stage>& v, hipStream_t s, hipEvent_t head_t0 = nullptr,
+                  hipEvent_t head_t1 = nullptr) {
+  for (const Stage& st : v) {
+    switch (st.kind) {
+      case ST_GEMV_NORM_1x8: QH_HIP(launch_gemv(st.g, 4, s)); break;
+      case ST_GEMV_GATED_2x4:
+      case ST_GEMV_LOAD_2x4:
+      case ST_GEMV_LOAD_4x4: QH_HIP(launch_gemv(st.g, 1, s)); break;
+      case ST_DELTANET: QH_HIP(launch_deltanet(st.d, s)); break;
+      case ST_ATTN: QH_HIP(launch_attn(st.at, s)); break;
+      case ST_COMBINE: QH_HIP(launch_attn_combine(st.at, s)); break;
+      default:
+        if (head_t0) QH_HIP(hipEventRecord(head_t0, s));
+        QH_HIP(launch_head(st.hd, e->head_grid, s));
+        if (head_t1) QH_HIP(hipEventRecord(head_t1, s));
+        QH_HIP(launch_argmax(e->part_val, e->part_idx, e->head_grid, e->ctl, nullptr, s));
+        break;
+    }
+  }
+  return QH_OK;
+}
+
+int enqueue_layers(qh_engine* e, int l0, int l1, bool embed, hipStream_t s) {
+  std::vector<Stage> v;
+  build_layers(e, l0, l1, embed, false, v);
+  return launch_stages(e, v, s);
+}
+
+// The persistent kernel's per-token program for the current mode.
+int ensure_prog(qh_engine* e) {
+  if (e->prog[e->mode]) return QH_OK;
+  std::vector<Stage> v;
+  build_layers(e, 0, kLayers, true, true, v);
+  Stage hd = head_stage(e, false);
+  hd.hd.done = nullptr;
+  v.push_back(hd);
+  QH_TRY(dalloc(&e->prog[e->mode], v.size()));
+  QH_HIP(hipMemcpy(e->prog[e->mode], v.data(), sizeof(Stage) * v.size(), hipMemcpyHostToDevice));
+  e->prog_n = (int)v.size();
+  return QH_OK;
+}
+
+// run_persist's answer when the cooperative launch itself is refused (the
+// device's cooperative resources can be held by another process): the engine
+// switches to the graph path, which runs the same kernels bit for bit.
+constexpr int kUseGraph = 1000;
+
+// One persistent launch: the prompt (already in prompt_dev) through the
+// run_hls loop, n_new greedy tokens at most, token feedback on the device.
+int run_persist(qh_engine* e, int tok0, int n_prompt, int n_new, int eos, bool with_logits, StepCtl* out) {
+  QH_TRY(ensure_prog(e));
+  hipStream_t s = e->stream;
+  StepCtl c;
+  std::memset(&c, 0, sizeof c);
+  c.tok = tok0;
+  c.pos = e->host_pos;
+  c.argmax = e->last_argmax;
+  c.n_prompt = n_prompt;
+  c.n_new = n_new;
+  c.eos = eos;
+  c.max_ctx = e->max_ctx;
+  QH_HIP(hipMemcpyAsync(e->ctl, &c, sizeof c, hipMemcpyHostToDevice, s));
+  QH_HIP(hipMemsetAsync(e->bar, 0, sizeof(unsigned) * (kBarCounters * kBarStride + 64), s));
+  PersistArgs a;
+  // QH_TRACE_FILE=path: barrier arrival / release times of every workgroup for
+  // the first two tokens of this launch, written as text (s_memrealtime ticks).
+  const char* trace_path = std::getenv("QH_TRACE_FILE");
+  uint64_t* trace = nullptr;
+  const int trace_bars = 2 * (e->prog_n + 1);
+  if (trace_path != nullptr && trace_path[0] != '\0') {
+    QH_TRY(dalloc(&trace, (size_t)trace_bars * e->persist_grid * 2));
+    QH_HIP(hipMemsetAsync(trace, 0, sizeof(uint64_t) * (size_t)trace_bars * e->persist_grid * 2, s));
+    a.trace = trace;
+    a.trace_bars = trace_bars;
+  }
+  a.prog = e->prog[e->mode];
+  a.nstage = e->prog_n;
+  a.mode = e->mode;
+  a.ctl = e->ctl;
+  a.prompt = e->prompt_dev;
+  a.out_ids = e->out_dev;
+  a.logits = with_logits ? e->logits : nullptr;
+  a.part_val = e->part_val;
+  a.part_idx = e->part_idx;
+  a.bar = e->bar;
+  a.abort_flag = reinterpret_cast<int*>(e->bar + kBarCounters * kBarStride);
+  if (launch_persist(a, e->persist_grid, s) != hipSuccess) {
+    (void)hipGetLastError();
+    if (trace != nullptr) (void)hipFree(trace);
+    e->persist_grid = 0;
+    e->exec = QH_EXEC_GRAPH;
+    return kUseGraph;
+  }
+  QH_HIP(hipMemcpyAsync(out, e->ctl, sizeof *out, hipMemcpyDeviceToHost, s));
+  QH_HIP(hipStreamSynchronize(s));
+  if (trace != nullptr) {
+    std::vector<uint64_t> h((size_t)trace_bars * e->persist_grid * 2);
+    const hipError_t ce = hipMemcpy(h.data(), trace, h.size() * sizeof(uint64_t), hipMemcpyDeviceToHost);
+    (void)hipFree(trace);
+    QH_HIP(ce);
+    if (FILE* f = std::fopen(trace_path, "w")) {
+      std::fprintf(f, "# barrier block arrive release (s_memrealtime ticks); %d stages per token\n", e->prog_n + 1);
+      for (int b = 0; b < trace_bars; ++b)
+        for (int k = 0; k < e->persist_grid; ++k)
+          std::fprintf(f, "%d %d %llu %llu\n", b, k, (unsigned long long)h[((size_t)b * e->persist_grid + k) * 2],
+                       (unsigned long long)h[((size_t)b * e->persist_grid + k) * 2 + 1]);
+      std::fclose(f);
+    }
+  }
+  e->host_pos = out->pos;
+  e->last_argmax = out->argmax;
+  if (out->err == 3) return QH_EDEVICE;
+  return QH_OK;
+}
+
+// One full decode step (qwen_top): embed, 24 layers, final norm, tied head,
+// argmax (+ pos), optionally the generation bookkeeping.
+int enqueue_step(qh_engine* e, bool with_logits, bool advance, hipStream_t s,
+                 hipEvent_t head_t0 = nullptr, hipEvent_t head_t1 = nullptr) {
+  std::vector<Stage> v;
+  build_layers(e, 0, kLayers, true, false, v);
+  v.push_back(head_stage(e, with_logits));
+  QH_TRY(launch_stages(e, v, s, head_t0, head_t1));
   if (advance) QH_HIP(launch_advance(e->ctl, e->prompt_dev, e->out_dev, s));
   return QH_OK;
 }
@@ -278,11 +435,6 @@ int get_graph(qh_engine* e, bool with_logits, bool advance, hipGraphExec_t* out)
   return QH_OK;
 }
 
-template <class T>
-int dalloc(T** p, size_t n) {
-  return hip_status(hipMalloc(reinterpret_cast<void**>(p), n * sizeof(T)));
-}
-
 void release(qh_engine* e) {
   if (!e) return;
   if (e->stream) (void)hipStreamSynchronize(e->stream);
@@ -292,7 +444,7 @@ void release(qh_engine* e) {
         if (g) (void)hipGraphExecDestroy(g);
   void* bufs[] = {e->blob, e->rec, e->conv, e->kc, e->vc, e->h, e->convd, e->zb, e->gb, e->o, e->act,
                   e->og, e->qg, e->kraw, e->vraw, e->pm, e->pl, e->pacc, e->rope, e->logits, e->part_val,
-                  e->part_idx, e->ctl, e->prompt_dev, e->out_dev};
+                  e->part_idx, e->ctl, e->prompt_dev, e->out_dev, e->prog[0], e->prog[1], e->bar};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -360,8 +512,11 @@ int create(const void* blob, size_t blob_len, const char* idx_text, int max_ctx,
   QH_C(dalloc(&e->pacc, (size_t)8 * e->nsplit_max * 256));
   QH_C(dalloc(&e->rope, (size_t)max_ctx * 64));
   QH_C(dalloc(&e->logits, kVocab));
-  QH_C(dalloc(&e->part_val, e->head_grid));
-  QH_C(dalloc(&e->part_idx, e->head_grid));
+  QH_C(dalloc(&e->part_val, e->head_grid > 256 ? e->head_grid : 256));
+  QH_C(dalloc(&e->part_idx, e->head_grid > 256 ? e->head_grid : 256));
+  QH_C(dalloc(&e->bar, kBarCounters * kBarStride + 64));
+  if (persist_max_grid(&e->persist_grid) != 0) e->persist_grid = 0;
+  if (e->persist_grid == 0) e->exec = QH_EXEC_GRAPH;
   QH_C(dalloc(&e->ctl, 1));
   {
     std::vector<float> rope((size_t)max_ctx * 64);
@@ -429,6 +584,15 @@ int qh_engine_set_mode(qh_engine* e, int mode) {
   return QH_OK;
 }
 
+int qh_engine_set_exec(qh_engine* e, int exec) {
+  if (!e || (exec != QH_EXEC_PERSISTENT && exec != QH_EXEC_GRAPH)) return QH_EINVAL;
+  if (exec == QH_EXEC_PERSISTENT && e->persist_grid == 0) return QH_ESTATE;
+  e->exec = exec;
+  return QH_OK;
+}
+
+int qh_engine_get_exec(const qh_engine* e) { return e ? e->exec : QH_EINVAL; }
+
 int qh_engine_reset(qh_engine* e) {
   if (!e) return QH_EINVAL;
   hipStream_t s = e->stream;
@@ -451,6 +615,17 @@ int qh_decode_token(qh_engine* e, int tok, float* logits, int* argmax_out) {
   if (!e || !argmax_out) return QH_EINVAL;
   if (tok < 0 || tok >= kVocab) return QH_ERANGE;
   if (e->host_pos >= e->max_ctx) return QH_ERANGE;
+  if (e->exec == QH_EXEC_PERSISTENT) {   // one token = a prompt of one, no new tokens
+    QH_HIP(hipMemcpyAsync(e->prompt_dev, &tok, sizeof(int), hipMemcpyHostToDevice, e->stream));
+    StepCtl c;
+    const int st = run_persist(e, tok, 1, 0, -1, logits != nullptr, &c);
+    if (st != kUseGraph) {
+      QH_TRY(st);
+      if (logits) QH_HIP(hipMemcpy(logits, e->logits, sizeof(float) * kVocab, hipMemcpyDeviceToHost));
+      *argmax_out = c.argmax;
+      return QH_OK;
+    }
+  }
   hipGraphExec_t g;
   QH_TRY(get_graph(e, logits != nullptr, false, &g));
   hipStream_t s = e->stream;
@@ -476,6 +651,17 @@ int qh_generate(qh_engine* e, const int* prompt, int n_prompt, int n_new, int eo
   hipStream_t s = e->stream;
   QH_HIP(hipMemcpyAsync(e->prompt_dev, prompt, sizeof(int) * (size_t)n_prompt, hipMemcpyHostToDevice, s));
   QH_HIP(hipStreamSynchronize(s));
+  if (e->exec == QH_EXEC_PERSISTENT) {
+    StepCtl c;
+    const int st = run_persist(e, prompt[0], n_prompt, n_new, eos, false, &c);
+    if (st != kUseGraph) {
+      QH_TRY(st);
+      if (c.n_out > 0)
+        QH_HIP(hipMemcpy(out_ids, e->out_dev, sizeof(int) * (size_t)c.n_out, hipMemcpyDeviceToHost));
+      *n_out = c.n_out;
+      return c.err == 2 ? QH_ERANGE : QH_OK;
+    }
+  }
   hipGraphExec_t g;
   QH_TRY(get_graph(e, false, true, &g));
   QH_HIP(launch_init_gen(e->ctl, prompt[0], n_prompt, n_new, eos, s));

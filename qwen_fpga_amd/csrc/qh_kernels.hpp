@@ -56,7 +56,8 @@ struct GemvArgs {
   float eps = 1e-6f;
   const int8_t* emb = nullptr;  // P_NORM: if set, x = emb[tok]*emb_s[tok] (gemv.hpp:76-84)
   const float* emb_s = nullptr;
-  const int* tok = nullptr;
+  const int* tok = nullptr;     // token id in device memory, or
+  int tokv = 0;                 // the token id itself when tok is null
   float* h_out = nullptr;       // receives the embedded row (block 0)
   const int* done = nullptr;    // engine stop flag (skip when *done != 0)
   int nseg = 0;
@@ -116,7 +117,23 @@ struct AttnArgs {
 
 struct DnArgs {
   const float* convd = nullptr;  // [6144] post-conv q | k | v
-  const float* gb = nullptr;     // g[16] then beta[16]
+  const float* gb = nullptr;     // g[16] then beta[16] (used when wa is null)
+  // Gate projections computed by each unit for its head (deltanet.hpp:164-165):
+  // beta = sigmoid(wb[h] . x), g = -exp(A_log[h]) * softplus(wa[h] . x + dt_bias[h]),
+  // x = the layer input (gx, rmsnorm'd with gx_norm when that is set; the
+  // embedded token when emb is set), int8-quantised and dequantised in W8A8 as
+  // the in_proj prologue does.  Reads only inputs that are final before in_proj.
+  const float* gx = nullptr;
+  const float* gx_norm = nullptr;
+  float eps = 1e-6f;
+  const float* wb = nullptr;     // fp32 [16][1024]
+  const float* wa = nullptr;     // fp32 [16][1024]
+  const float* A_log = nullptr;
+  const float* dt_bias = nullptr;
+  const int8_t* emb = nullptr;
+  const float* emb_s = nullptr;
+  const int* tok = nullptr;      // token id in device memory (null: passed by the caller)
+  int mode = M_W8A16;
   float* S = nullptr;            // [16][128][128]
   float* o = nullptr;            // [16][128]
   int normalize = 1;             // l2norm q,k and scale q (0: given already normalized)
@@ -125,6 +142,50 @@ struct DnArgs {
 };
 
 struct Floats64 { float v[64]; };
+
+// One stage of the persistent decode kernel: the arguments a per-stage kernel
+// would get, and which body runs them.
+enum StageKind : int {
+  ST_GEMV_NORM_1x8 = 0,    // gemv_body<1, mode, P_NORM, 8>   in_proj / q,k,v / gate,up
+  ST_GEMV_GATED_2x4 = 1,   // gemv_body<2, mode, P_GATED, 4>  DeltaNet out_proj
+  ST_GEMV_LOAD_2x4 = 2,    // gemv_body<2, mode, P_LOAD, 4>   attention o_proj
+  ST_GEMV_LOAD_4x4 = 3,    // gemv_body<4, mode, P_LOAD, 4>   MLP down
+  ST_DELTANET = 4,
+  ST_ATTN = 5,
+  ST_COMBINE = 6,
+  ST_HEAD = 7,
+};
+struct Stage {
+  int kind = ST_GEMV_NORM_1x8;
+  GemvArgs g;
+  DnArgs d;
+  AttnArgs at;
+  HeadArgs hd;
+};
+
+// Persistent decode: prog[0..nstage) is one token (embed .. LM head).  The
+// kernel runs tokens until the run_hls loop of StepCtl stops it.
+struct PersistArgs {
+  const Stage* prog = nullptr;
+  int nstage = 0;
+  int mode = M_W8A16;
+  StepCtl* ctl = nullptr;       // in: tok, pos, step, n_prompt, n_new, n_out, eos, max_ctx; out: all
+  const int* prompt = nullptr;  // [n_prompt]
+  int* out_ids = nullptr;       // [n_new]
+  float* logits = nullptr;      // optional: logits of every step (the last one remains)
+  float* part_val = nullptr;    // [grid] LM-head partial maxima
+  int* part_idx = nullptr;
+  unsigned* bar = nullptr;      // grid-barrier counters (zeroed before launch)
+  int* abort_flag = nullptr;    // set when a barrier wait exceeds its spin limit
+  uint64_t* trace = nullptr;    // optional [trace_bars][grid][2]: arrival / release time per barrier
+  int trace_bars = 0;
+};
+constexpr int kBarCounters = 16;      // arrival counters (workgroup b counts on b % 16)
+constexpr int kBarStride = 64;        // uints between counters (256 B)
+constexpr int kPersistThreads = 256;
+
+hipError_t launch_persist(const PersistArgs& a, int grid, hipStream_t s);
+int persist_max_grid(int* grid);   // workgroups the cooperative launch can hold (a multiple of 16)
 
 // ---- launch wrappers (return hipError_t) ----
 hipError_t launch_gemv(const GemvArgs& a, int waves_per_block, hipStream_t s);

@@ -4,6 +4,8 @@
 // intermediate buffers take them from the stream-ordered allocator
 // (hipMallocAsync / hipFreeAsync on the same stream), so they stay reentrant.
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "qh_common.hpp"
@@ -21,6 +23,16 @@ void rope_row(int pos, float* out64) {
     out64[j] = std::cos(f);
     out64[32 + j] = std::sin(f);
   }
+}
+
+int hip_report(hipError_t e, const char* what, const char* file, int line) {
+  if (e == hipSuccess) return QH_OK;
+  static const bool verbose = [] {
+    const char* v = std::getenv("QH_VERBOSE");
+    return v != nullptr && v[0] != '\0' && v[0] != '0';
+  }();
+  if (verbose) std::fprintf(stderr, "[qh] %s:%d: %s -> %s (%d)\n", file, line, what, hipGetErrorString(e), (int)e);
+  return (int)e;
 }
 
 }  // namespace qh
@@ -90,10 +102,9 @@ int deltanet_layer(float* out, const float* x, const qh_tensor* qkv_w, const qh_
     return QH_EINVAL;
   if (!aligned16(x) || !aligned16(gate_norm_w)) return QH_EINVAL;
   Scratch sc(s);
-  QH_TRY(sc.alloc(rnd(4 * kConvDim) + rnd(4 * kZDim) + rnd(4 * 32) + rnd(4 * kLH * kLV)));
+  QH_TRY(sc.alloc(rnd(4 * kConvDim) + rnd(4 * kZDim) + rnd(4 * kLH * kLV)));
   float* convd = sc.take<float>(kConvDim);
   float* zb = sc.take<float>(kZDim);
-  float* gb = sc.take<float>(32);
   float* o = sc.take<float>(kLH * kLV);
   // in_proj_qkv / z / b / a over the shared activation (deltanet.hpp:149-152, model.py:143-147)
   GemvArgs a;
@@ -101,36 +112,22 @@ int deltanet_layer(float* out, const float* x, const qh_tensor* qkv_w, const qh_
   a.mode = mode;
   a.prologue = P_LOAD;
   a.x = x;
-  a.nseg = 4;
+  a.nseg = 2;   // the fp32 gate projections b, a run in the DeltaNet stage
   int b0 = 0;
   a.seg[0] = seg_i8(qkv_w->w_i8, qkv_w->scale, kConvDim, b0, convd, E_CONV);
   a.seg[0].c0 = conv_w;
   a.seg[0].c2 = conv_state;
   b0 += a.seg[0].nbatch;
   a.seg[1] = seg_i8(z_w->w_i8, z_w->scale, kZDim, b0, zb, E_SILU);   // silu(z) for the gated norm
-  b0 += a.seg[1].nbatch;
-  Seg gbeta;
-  gbeta.kind = SEG_F32;
-  gbeta.epi = E_GATE_B;
-  gbeta.batch0 = b0;
-  gbeta.rows = kLH;
-  gbeta.nbatch = kLH / kRowsPerBatch;
-  gbeta.wf = b_w->w_f32;
-  gbeta.out = gb + 16;
-  a.seg[2] = gbeta;
-  b0 += gbeta.nbatch;
-  Seg ga = gbeta;
-  ga.epi = E_GATE_A;
-  ga.batch0 = b0;
-  ga.wf = a_w->w_f32;
-  ga.out = gb;
-  ga.c0 = A_log;
-  ga.c1 = dt_bias;
-  a.seg[3] = ga;
   QH_HIP(launch_gemv(a, 4, s));
-  DnArgs d;
+  DnArgs d;   // gates (deltanet.hpp:164-165) on x itself, l2norm, delta rule
   d.convd = convd;
-  d.gb = gb;
+  d.gx = x;
+  d.wb = b_w->w_f32;
+  d.wa = a_w->w_f32;
+  d.A_log = A_log;
+  d.dt_bias = dt_bias;
+  d.mode = mode;
   d.S = rec;
   d.o = o;
   QH_HIP(launch_deltanet(d, s));
@@ -269,6 +266,7 @@ const char* qh_strerror(int st) {
     case QH_EFORMAT: return "weight index or blob does not match the packed layout";
     case QH_ENOMEM: return "allocation failed";
     case QH_ESTATE: return "engine state does not allow the call";
+    case QH_EDEVICE: return "device-side wait timed out";
     default: return st > 0 ? hipGetErrorString((hipError_t)st) : "unknown status";
   }
 }

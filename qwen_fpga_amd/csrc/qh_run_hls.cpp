@@ -81,9 +81,11 @@ int main(int argc, char** argv) {
   }
   for (size_t i = 0; i < gen.size(); ++i) std::printf("%d%s", gen[i], i + 1 < gen.size() ? " " : "\n");
   const double pf = ms(t0, t1), dc = ms(t1, t2);
-  std::fprintf(stderr, "[mi355x] prefill %zu tok %.1f ms (%.1f tok/s) | decode %zu tok %.1f ms (%.1f tok/s)\n",
+  std::fprintf(stderr,
+               "[mi355x] prefill %zu tok %.1f ms (%.1f tok/s) | decode %zu tok %.1f ms (%.1f tok/s) | %s\n",
                prompt.size(), pf, prompt.size() / (pf / 1000.0), gen.size(), dc,
-               gen.empty() ? 0.0 : gen.size() / (dc / 1000.0));
+               gen.empty() ? 0.0 : gen.size() / (dc / 1000.0),
+               qh_engine_get_exec(e) == QH_EXEC_PERSISTENT ? "persistent kernel" : "graph per token");
   qh_engine_destroy(e);
   return 0;
 }

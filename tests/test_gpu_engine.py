@@ -71,6 +71,31 @@ def test_decode_matches_device_twin(q, orc, engine, model, mode):
     assert_bitwise(d2h(engine.device_ptr(4), (6, 64, 512))[:, :len(toks)], model.vcache()[:, :len(toks)], "v cache")
 
 
+@pytest.mark.parametrize("mode", [0, 1], ids=["w8a16", "w8a8"])
+def test_persistent_equals_graph_path(q, engine, mode):
+    """The persistent kernel (one launch, grid barriers) and the per-stage graph give the same bits."""
+    default = engine.exec_kind
+    engine.set_mode(mode)
+    toks = [5, 248319, 17, 0, 99999, 3]
+    runs = []
+    for ex in (q.EXEC_GRAPH, q.EXEC_PERSISTENT):
+        engine.set_exec(ex)
+        engine.reset()
+        lg_all = [engine.decode_token(t, want_logits=True)[1] for t in toks]
+        st = (d2h(engine.device_ptr(1), (18, 16, 128, 128)), d2h(engine.device_ptr(2), (18, 6144, 4)),
+              d2h(engine.device_ptr(3), (6, 64, 512)), d2h(engine.device_ptr(4), (6, 64, 512)))
+        engine.reset()
+        gen = engine.generate([11, 2222, 33333], 20)
+        runs.append((lg_all, st, gen, engine.pos))
+    engine.set_exec(default)
+    (lg_g, st_g, gen_g, pos_g), (lg_p, st_p, gen_p, pos_p) = runs
+    for i, (a, b) in enumerate(zip(lg_g, lg_p)):
+        assert_bitwise(b, a, f"logits step {i}")
+    for name, a, b in zip(("rec", "conv", "k", "v"), st_g, st_p):
+        assert_bitwise(b, a, name)
+    assert gen_p == gen_g and pos_p == pos_g == 23
+
+
 def test_reset_restarts_the_sequence(engine):
     engine.set_mode(0)
     engine.reset()
