@@ -45,6 +45,9 @@ def main() -> int:
     ap.add_argument("--cpu-tokens", type=int, default=8, help="reference CPU decode sample (tokens)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-steps", type=int, default=16)
+    ap.add_argument("--exec", dest="exec_kind", choices=["graph", "persistent"], default="graph",
+                    help="graph: one hipGraph of per-stage kernels per token; persistent: one cooperative "
+                         "launch runs every token with grid barriers between stages")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build runs batch-1 decode on a single MI355X "
@@ -64,6 +67,7 @@ def main() -> int:
     mode = q.MODE_W8A8 if args.mode == "w8a8" else q.MODE_W8A16
     max_ctx = args.prompt + max(args.steps, args.warmup) + args.profile_steps + 2
     eng = q.Engine(blob, idx=idx, max_ctx=max_ctx, mode=mode)
+    eng.set_exec(q.EXEC_PERSISTENT if args.exec_kind == "persistent" else q.EXEC_GRAPH)
 
     # warmup: graph instantiation + a short run from a fresh state
     eng.reset()
@@ -110,6 +114,8 @@ def main() -> int:
                         f"{args.prompt}-token prompt then {args.steps} greedy steps (KV to "
                         f"{args.prompt + args.steps})",
             "act_mode": args.mode,
+            "exec": args.exec_kind if eng.exec_kind == (q.EXEC_PERSISTENT if args.exec_kind == "persistent"
+                                                         else q.EXEC_GRAPH) else "graph (fallback)",
             "bytes_per_token_floor": FLOOR_BYTES,
             "bytes_per_token_full_mean": int(mean_full),
         },
