@@ -61,12 +61,16 @@ struct qh_engine {
   int last_argmax = -1;
   // graphs[mode][logits][advance]
   hipGraphExec_t graphs[2][2][2] = {};
-  // persistent path: the per-token stage program per mode, barrier counters
+  // persistent path: the per-token stage program per mode over the tagged
+  // hand-over arena (every stage output its own region of 8-byte pairs)
   int exec = QH_EXEC_GRAPH;
   int persist_grid = 0;          // 0: cooperative launch not available (graph path only)
   Stage* prog[2] = {};
   int prog_n = 0;
-  unsigned* bar = nullptr;       // kBarCounters * kBarStride counters + abort flag
+  uint64_t* arena = nullptr;     // tagged vectors of the persistent program
+  size_t arena_pairs = 0;
+  uint32_t tag_next = 1;         // first unused tag (the arena holds only smaller tags)
+  int* abort_dev = nullptr;      // set by a hand-over wait that gave up
 };
 
 namespace {
@@ -90,6 +94,7 @@ Seg mkseg(int kind, int epi, int rows, int batch0, float* out, int rpb = kRowsPe
   g.batch0 = batch0;
   g.nbatch = (rows + rpb - 1) / rpb;
   g.out = out;
+  g.res = out;
   return g;
 }
 
@@ -105,44 +110,78 @@ Stage gemv_stage(int kind, const GemvArgs& a) {
   return st;
 }
 
-// The stages of layers [l0, l1) of one decode step on the residual stream
-// e->h.  `persistent` leaves the device StepCtl pointers out: the persistent
-// kernel passes the token and position itself and stops at its own barrier.
-void build_layers(const qh_engine* e, int l0, int l1, bool embed, bool persistent, std::vector<Stage>& out) {
-  const int* done = persistent ? nullptr : &e->ctl->done;
+// Output vectors of the stages.  Plain (graph engine): the engine's fixed
+// activation buffers, the residual stream updated in place.  Tagged
+// (persistent kernel): a fresh region of the arena for every stage output, so
+// no vector is written twice within a token.  With arena == nullptr the tagged
+// form only counts pairs.
+struct Bufs {
+  bool tagged = false;
+  uint64_t* arena = nullptr;
+  size_t used = 0;   // pairs
+  float* take(size_t n, float* plain) {
+    if (!tagged) return plain;
+    const size_t off = used;
+    used += (n + 31) & ~(size_t)31;   // 256-byte aligned regions
+    return arena != nullptr ? reinterpret_cast<float*>(arena + off) : nullptr;
+  }
+};
+
+// A hand-over vector and the stage that produces it.
+struct Vec {
+  float* p = nullptr;
+  int st = 0;
+};
+
+// The stages of layers [l0, l1) of one decode step on the residual stream h
+// (updated to the last stage's output).  The tagged program leaves the device
+// StepCtl pointers out: the persistent kernel passes the token and position
+// itself.
+void build_layers(const qh_engine* e, int l0, int l1, bool embed, Bufs& B, std::vector<Stage>& out, Vec& h) {
+  const bool tag = B.tagged;
+  const int* done = tag ? nullptr : &e->ctl->done;
   int li = 0, fi = 0;
   for (int l = 0; l < l0; ++l) (is_linear(l) ? li : fi)++;
   for (int l = l0; l < l1; ++l) {
     if (is_linear(l)) {
-      // in_ln rmsnorm (+ act-quant) -> qkv(conv+SiLU) | z | beta | g   (deltanet.hpp:149-165)
+      // in_ln rmsnorm (+ act-quant) -> qkv(conv+SiLU) | z   (deltanet.hpp:149-165)
+      const int sA = (int)out.size();
       GemvArgs a;
       a.K = kHidden;
       a.mode = e->mode;
       a.prologue = P_NORM;
-      a.x = e->h;
+      a.x = h.p;
+      a.x_st = h.st;
+      a.out_st = sA;
       a.nw = f32p(e, l, R_IN_LN);
       a.eps = kEps;
       a.done = done;
+      float* convd = B.take(kConvDim, e->convd);
+      float* zb = B.take(kZDim, e->zb);
       if (embed && l == l0) {   // embed_row (qwen_synth.hpp:42-43), written to the residual
         a.emb = i8p(e, kLayers, R_EMBED);
         a.emb_s = scp(e, kLayers, R_EMBED);
-        a.tok = persistent ? nullptr : &e->ctl->tok;
-        a.h_out = e->h;
+        a.tok = tag ? nullptr : &e->ctl->tok;
+        a.h_out = B.take(kHidden, e->h);
+        h = Vec{a.h_out, sA};
       }
       a.nseg = 2;   // the fp32 gate projections b, a run in the DeltaNet stage
-      a.seg[0] = mkseg(SEG_I8, E_CONV, kConvDim, 0, e->convd);
+      a.seg[0] = mkseg(SEG_I8, E_CONV, kConvDim, 0, convd);
       a.seg[0].w = i8p(e, l, R_QKV);
       a.seg[0].sw = scp(e, l, R_QKV);
       a.seg[0].c0 = f32p(e, l, R_CONV);
       a.seg[0].c2 = e->conv + (size_t)li * kConvDim * kConvK;
-      a.seg[1] = mkseg(SEG_I8, E_SILU, kZDim, a.seg[0].nbatch, e->zb);   // silu(z) for the gated norm
+      a.seg[1] = mkseg(SEG_I8, E_SILU, kZDim, a.seg[0].nbatch, zb);   // silu(z) for the gated norm
       a.seg[1].w = i8p(e, l, R_Z);
       a.seg[1].sw = scp(e, l, R_Z);
       out.push_back(gemv_stage(ST_GEMV_NORM_1x8, a));
+      const int sB = (int)out.size();
       DnArgs d;   // gates b, a (deltanet.hpp:164-165), l2norm, delta rule (deltanet.hpp:166-173)
-      d.convd = e->convd;
+      d.convd = convd;
+      d.convd_st = sA;
       d.gb = e->gb;
-      d.gx = e->h;
+      d.gx = h.p;
+      d.gx_st = h.st;
       d.gx_norm = f32p(e, l, R_IN_LN);
       d.eps = kEps;
       d.wb = f32p(e, l, R_B);
@@ -153,68 +192,83 @@ void build_layers(const qh_engine* e, int l0, int l1, bool embed, bool persisten
       if (embed && l == l0) {   // layer 0 reads the embedded token, not the residual
         d.emb = i8p(e, kLayers, R_EMBED);
         d.emb_s = scp(e, kLayers, R_EMBED);
-        d.tok = persistent ? nullptr : &e->ctl->tok;
+        d.tok = tag ? nullptr : &e->ctl->tok;
       }
       d.S = e->rec + (size_t)li * kLH * kLK * kLV;
-      d.o = e->o;
+      d.o = B.take(kLH * kLV, e->o);
+      d.o_st = sB;
       d.done = done;
       Stage sd;
       sd.kind = ST_DELTANET;
       sd.d = d;
       out.push_back(sd);
+      const int sC = (int)out.size();
       GemvArgs c;   // gated rmsnorm (+ quant) -> out_proj, residual add (deltanet.hpp:177-181)
       c.K = kLH * kLV;
       c.mode = e->mode;
       c.prologue = P_GATED;
-      c.x = e->o;
+      c.x = d.o;
+      c.x_st = sB;
       c.nw = f32p(e, l, R_LNORM);
-      c.z = e->zb;
+      c.z = zb;
+      c.z_st = sA;
+      c.out_st = sC;
       c.eps = kEps;
       c.done = done;
       c.nseg = 1;
-      c.rows_per_batch = 4;
-      c.seg[0] = mkseg(SEG_I8, E_RESID, kHidden, 0, e->h, 4);
+      c.rows_per_batch = 1;
+      c.seg[0] = mkseg(SEG_I8, E_RESID, kHidden, 0, B.take(kHidden, e->h), 1);
+      c.seg[0].res = h.p;
+      c.seg[0].res_st = h.st;
       c.seg[0].w = i8p(e, l, R_OUTP);
       c.seg[0].sw = scp(e, l, R_OUTP);
-      out.push_back(gemv_stage(ST_GEMV_GATED_2x4, c));
+      out.push_back(gemv_stage(ST_GEMV_GATED_2x1, c));
+      h = Vec{c.seg[0].out, sC};
       ++li;
     } else {
+      const int sA = (int)out.size();
       GemvArgs a;   // in_ln rmsnorm (+ quant) -> q||gate, k, v (attention.hpp:31-33)
       a.K = kHidden;
       a.mode = e->mode;
       a.prologue = P_NORM;
-      a.x = e->h;
+      a.x = h.p;
+      a.x_st = h.st;
+      a.out_st = sA;
       a.nw = f32p(e, l, R_IN_LN);
       a.eps = kEps;
       a.done = done;
       a.nseg = 3;
-      a.seg[0] = mkseg(SEG_I8, E_STORE, kQProj, 0, e->qg);
+      a.seg[0] = mkseg(SEG_I8, E_STORE, kQProj, 0, B.take(kQProj, e->qg));
       a.seg[0].w = i8p(e, l, R_QP);
       a.seg[0].sw = scp(e, l, R_QP);
-      a.seg[1] = mkseg(SEG_I8, E_STORE, kKVProj, a.seg[0].nbatch, e->kraw);
+      a.seg[1] = mkseg(SEG_I8, E_STORE, kKVProj, a.seg[0].nbatch, B.take(kKVProj, e->kraw));
       a.seg[1].w = i8p(e, l, R_KP);
       a.seg[1].sw = scp(e, l, R_KP);
-      a.seg[2] = mkseg(SEG_I8, E_STORE, kKVProj, a.seg[1].batch0 + a.seg[1].nbatch, e->vraw);
+      a.seg[2] = mkseg(SEG_I8, E_STORE, kKVProj, a.seg[1].batch0 + a.seg[1].nbatch, B.take(kKVProj, e->vraw));
       a.seg[2].w = i8p(e, l, R_VP);
       a.seg[2].sw = scp(e, l, R_VP);
       out.push_back(gemv_stage(ST_GEMV_NORM_1x8, a));
+      const int sB = (int)out.size();
       AttnArgs at;
-      at.qg = e->qg;
-      at.kraw = e->kraw;
-      at.vraw = e->vraw;
+      at.qg = a.seg[0].out;
+      at.kraw = a.seg[1].out;
+      at.vraw = a.seg[2].out;
+      at.qkv_st = sA;
       at.qn = f32p(e, l, R_QN);
       at.kn = f32p(e, l, R_KN);
       at.rope = e->rope;
       at.kc = e->kc + (size_t)fi * e->max_ctx * kKVProj;
       at.vc = e->vc + (size_t)fi * e->max_ctx * kKVProj;
-      at.T = persistent ? nullptr : &e->ctl->pos;
-      at.rope_row = persistent ? nullptr : &e->ctl->pos;
-      at.pm = e->pm;
-      at.pl = e->pl;
-      at.pacc = e->pacc;
+      at.T = tag ? nullptr : &e->ctl->pos;
+      at.rope_row = tag ? nullptr : &e->ctl->pos;
+      at.pm = B.take((size_t)8 * e->nsplit_max, e->pm);
+      at.pl = B.take((size_t)8 * e->nsplit_max, e->pl);
+      at.pacc = B.take((size_t)8 * e->nsplit_max * 256, e->pacc);
+      at.part_st = sB;
       at.nsplit_max = e->nsplit_max;
       at.max_ctx = e->max_ctx;
-      at.og = e->og;
+      at.og = B.take(kNH * kHD, e->og);
+      at.og_st = sB + 1;
       at.eps = kEps;
       at.done = done;
       Stage sa;
@@ -223,66 +277,83 @@ void build_layers(const qh_engine* e, int l0, int l1, bool embed, bool persisten
       out.push_back(sa);
       sa.kind = ST_COMBINE;
       out.push_back(sa);
+      const int sC = (int)out.size();
       GemvArgs c;   // (+ quant) o_proj, residual add (attention.hpp:94)
       c.K = kNH * kHD;
       c.mode = e->mode;
       c.prologue = P_LOAD;
-      c.x = e->og;
+      c.x = at.og;
+      c.x_st = at.og_st;
+      c.out_st = sC;
       c.done = done;
       c.nseg = 1;
-      c.rows_per_batch = 4;
-      c.seg[0] = mkseg(SEG_I8, E_RESID, kHidden, 0, e->h, 4);
+      c.rows_per_batch = 1;
+      c.seg[0] = mkseg(SEG_I8, E_RESID, kHidden, 0, B.take(kHidden, e->h), 1);
+      c.seg[0].res = h.p;
+      c.seg[0].res_st = h.st;
       c.seg[0].w = i8p(e, l, R_OP);
       c.seg[0].sw = scp(e, l, R_OP);
-      out.push_back(gemv_stage(ST_GEMV_LOAD_2x4, c));
+      out.push_back(gemv_stage(ST_GEMV_LOAD_2x1, c));
+      h = Vec{c.seg[0].out, sC};
       ++fi;
     }
     // post_ln rmsnorm (+ quant) -> gate||up pairs with SwiGLU -> down, residual (mlp.hpp:11-19)
+    const int sD = (int)out.size();
     GemvArgs m;
     m.K = kHidden;
     m.mode = e->mode;
     m.prologue = P_NORM;
-    m.x = e->h;
+    m.x = h.p;
+    m.x_st = h.st;
+    m.out_st = sD;
     m.nw = f32p(e, l, R_POST_LN);
     m.eps = kEps;
     m.done = done;
     m.nseg = 1;
-    m.seg[0] = mkseg(SEG_PAIR, E_SWIGLU, 2 * kInter, 0, e->act);
+    m.seg[0] = mkseg(SEG_PAIR, E_SWIGLU, 2 * kInter, 0, B.take(kInter, e->act));
     m.seg[0].w = i8p(e, l, R_GATE);
     m.seg[0].sw = scp(e, l, R_GATE);
     m.seg[0].w2 = i8p(e, l, R_UP);
     m.seg[0].sw2 = scp(e, l, R_UP);
     out.push_back(gemv_stage(ST_GEMV_NORM_1x8, m));
+    const int sE = (int)out.size();
     GemvArgs dn;
     dn.K = kInter;
     dn.mode = e->mode;
     dn.prologue = P_LOAD;
-    dn.x = e->act;
+    dn.x = m.seg[0].out;
+    dn.x_st = sD;
+    dn.out_st = sE;
     dn.done = done;
     dn.nseg = 1;
-    dn.rows_per_batch = 4;
-    dn.seg[0] = mkseg(SEG_I8, E_RESID, kHidden, 0, e->h, 4);
+    dn.rows_per_batch = 1;
+    dn.seg[0] = mkseg(SEG_I8, E_RESID, kHidden, 0, B.take(kHidden, e->h), 1);
+    dn.seg[0].res = h.p;
+    dn.seg[0].res_st = h.st;
     dn.seg[0].w = i8p(e, l, R_DOWN);
     dn.seg[0].sw = scp(e, l, R_DOWN);
-    out.push_back(gemv_stage(ST_GEMV_LOAD_4x4, dn));
+    out.push_back(gemv_stage(ST_GEMV_LOAD_4x1, dn));
+    h = Vec{dn.seg[0].out, sE};
   }
 }
 
 // Final norm + tied LM head (qwen_synth.hpp:74-88).
-Stage head_stage(const qh_engine* e, bool with_logits) {
+Stage head_stage(const qh_engine* e, Bufs& B, const Vec& h, bool with_logits, int st_self, int nparts) {
   Stage st;
   st.kind = ST_HEAD;
   HeadArgs& hd = st.hd;
-  hd.h = e->h;
+  hd.h = h.p;
+  hd.h_st = h.st;
   hd.nw = f32p(e, kLayers, R_FINAL);
   hd.eps = kEps;
   hd.w = i8p(e, kLayers, R_EMBED);
   hd.sw = scp(e, kLayers, R_EMBED);
   hd.rows = kVocab;
   hd.logits = with_logits ? e->logits : nullptr;
-  hd.part_val = e->part_val;
-  hd.part_idx = e->part_idx;
-  hd.done = &e->ctl->done;
+  hd.part_val = B.take(nparts, e->part_val);
+  hd.part_idx = reinterpret_cast<int*>(B.take(nparts, reinterpret_cast<float*>(e->part_idx)));
+  hd.part_st = st_self;
+  hd.done = B.tagged ? nullptr : &e->ctl->done;
   return st;
 }
 
@@ -292,10 +363,10 @@ int launch_stages(qh_engine* e, const std::vector<Stage>& v, hipStream_t s, hipE
                   hipEvent_t head_t1 = nullptr) {
   for (const Stage& st : v) {
     switch (st.kind) {
-      case ST_GEMV_NORM_1x8: QH_HIP(launch_gemv(st.g, 4, s)); break;
-      case ST_GEMV_GATED_2x4:
-      case ST_GEMV_LOAD_2x4:
-      case ST_GEMV_LOAD_4x4: QH_HIP(launch_gemv(st.g, 1, s)); break;
+      case ST_GEMV_NORM_1x8:
+      case ST_GEMV_GATED_2x1:
+      case ST_GEMV_LOAD_2x1:
+      case ST_GEMV_LOAD_4x1: QH_HIP(launch_gemv(st.g, 4, s)); break;
       case ST_DELTANET: QH_HIP(launch_deltanet(st.d, s)); break;
       case ST_ATTN: QH_HIP(launch_attn(st.at, s)); break;
       case ST_COMBINE: QH_HIP(launch_attn_combine(st.at, s)); break;
@@ -312,18 +383,36 @@ int launch_stages(qh_engine* e, const std::vector<Stage>& v, hipStream_t s, hipE
 
 int enqueue_layers(qh_engine* e, int l0, int l1, bool embed, hipStream_t s) {
   std::vector<Stage> v;
-  build_layers(e, l0, l1, embed, false, v);
+  Bufs B;
+  Vec h{e->h, 0};
+  build_layers(e, l0, l1, embed, B, v, h);
   return launch_stages(e, v, s);
 }
 
-// The persistent kernel's per-token program for the current mode.
+// The persistent kernel's per-token program for the current mode, over the
+// tagged arena (allocated and zeroed on first use; both modes share it).
 int ensure_prog(qh_engine* e) {
   if (e->prog[e->mode]) return QH_OK;
   std::vector<Stage> v;
-  build_layers(e, 0, kLayers, true, true, v);
-  Stage hd = head_stage(e, false);
-  hd.hd.done = nullptr;
-  v.push_back(hd);
+  Vec h;
+  if (e->arena == nullptr) {
+    Bufs cnt;
+    cnt.tagged = true;
+    build_layers(e, 0, kLayers, true, cnt, v, h);
+    (void)head_stage(e, cnt, h, false, (int)v.size(), e->persist_grid);
+    QH_TRY(dalloc(&e->arena, cnt.used));
+    QH_HIP(hipMemset(e->arena, 0, sizeof(uint64_t) * cnt.used));
+    e->arena_pairs = cnt.used;
+    e->tag_next = 1;
+    v.clear();
+    h = Vec{};
+  }
+  Bufs B;
+  B.tagged = true;
+  B.arena = e->arena;
+  build_layers(e, 0, kLayers, true, B, v, h);
+  v.push_back(head_stage(e, B, h, false, (int)v.size(), e->persist_grid));
+  if ((int)v.size() >= kTagsPerToken || B.used != e->arena_pairs) return QH_ESTATE;
   QH_TRY(dalloc(&e->prog[e->mode], v.size()));
   QH_HIP(hipMemcpy(e->prog[e->mode], v.data(), sizeof(Stage) * v.size(), hipMemcpyHostToDevice));
   e->prog_n = (int)v.size();
@@ -340,6 +429,12 @@ constexpr int kUseGraph = 1000;
 int run_persist(qh_engine* e, int tok0, int n_prompt, int n_new, int eos, bool with_logits, StepCtl* out) {
   QH_TRY(ensure_prog(e));
   hipStream_t s = e->stream;
+  // tags of this launch: tag_base + k * kTagsPerToken + stage, k < n_prompt + n_new
+  const uint64_t need = ((uint64_t)n_prompt + (uint64_t)n_new + 1) * kTagsPerToken;
+  if ((uint64_t)e->tag_next + need > 0xFFFFFFFFull) {   // tags would wrap: clear the arena
+    QH_HIP(hipMemsetAsync(e->arena, 0, sizeof(uint64_t) * e->arena_pairs, s));
+    e->tag_next = 1;
+  }
   StepCtl c;
   std::memset(&c, 0, sizeof c);
   c.tok = tok0;
@@ -350,30 +445,29 @@ int run_persist(qh_engine* e, int tok0, int n_prompt, int n_new, int eos, bool w
   c.eos = eos;
   c.max_ctx = e->max_ctx;
   QH_HIP(hipMemcpyAsync(e->ctl, &c, sizeof c, hipMemcpyHostToDevice, s));
-  QH_HIP(hipMemsetAsync(e->bar, 0, sizeof(unsigned) * (kBarCounters * kBarStride + 64), s));
+  QH_HIP(hipMemsetAsync(e->abort_dev, 0, sizeof(int), s));
   PersistArgs a;
-  // QH_TRACE_FILE=path: barrier arrival / release times of every workgroup for
+  // QH_TRACE_FILE=path: completion time of every stage on every workgroup for
   // the first two tokens of this launch, written as text (s_memrealtime ticks).
   const char* trace_path = std::getenv("QH_TRACE_FILE");
   uint64_t* trace = nullptr;
-  const int trace_bars = 2 * (e->prog_n + 1);
+  const int trace_tokens = 2;
+  const size_t trace_n = (size_t)trace_tokens * e->prog_n * e->persist_grid * 4;
   if (trace_path != nullptr && trace_path[0] != '\0') {
-    QH_TRY(dalloc(&trace, (size_t)trace_bars * e->persist_grid * 2));
-    QH_HIP(hipMemsetAsync(trace, 0, sizeof(uint64_t) * (size_t)trace_bars * e->persist_grid * 2, s));
+    QH_TRY(dalloc(&trace, trace_n));
+    QH_HIP(hipMemsetAsync(trace, 0, sizeof(uint64_t) * trace_n, s));
     a.trace = trace;
-    a.trace_bars = trace_bars;
+    a.trace_tokens = trace_tokens;
   }
   a.prog = e->prog[e->mode];
   a.nstage = e->prog_n;
   a.mode = e->mode;
+  a.tag_base = e->tag_next;
   a.ctl = e->ctl;
   a.prompt = e->prompt_dev;
   a.out_ids = e->out_dev;
   a.logits = with_logits ? e->logits : nullptr;
-  a.part_val = e->part_val;
-  a.part_idx = e->part_idx;
-  a.bar = e->bar;
-  a.abort_flag = reinterpret_cast<int*>(e->bar + kBarCounters * kBarStride);
+  a.abort_flag = e->abort_dev;
   if (launch_persist(a, e->persist_grid, s) != hipSuccess) {
     (void)hipGetLastError();
     if (trace != nullptr) (void)hipFree(trace);
@@ -381,25 +475,35 @@ int run_persist(qh_engine* e, int tok0, int n_prompt, int n_new, int eos, bool w
     e->exec = QH_EXEC_GRAPH;
     return kUseGraph;
   }
+  e->tag_next += (uint32_t)need;
+  int aborted = 0;
   QH_HIP(hipMemcpyAsync(out, e->ctl, sizeof *out, hipMemcpyDeviceToHost, s));
+  QH_HIP(hipMemcpyAsync(&aborted, e->abort_dev, sizeof(int), hipMemcpyDeviceToHost, s));
   QH_HIP(hipStreamSynchronize(s));
   if (trace != nullptr) {
-    std::vector<uint64_t> h((size_t)trace_bars * e->persist_grid * 2);
-    const hipError_t ce = hipMemcpy(h.data(), trace, h.size() * sizeof(uint64_t), hipMemcpyDeviceToHost);
+    std::vector<uint64_t> hbuf(trace_n);
+    const hipError_t ce = hipMemcpy(hbuf.data(), trace, trace_n * sizeof(uint64_t), hipMemcpyDeviceToHost);
     (void)hipFree(trace);
     QH_HIP(ce);
     if (FILE* f = std::fopen(trace_path, "w")) {
-      std::fprintf(f, "# barrier block arrive release (s_memrealtime ticks); %d stages per token\n", e->prog_n + 1);
-      for (int b = 0; b < trace_bars; ++b)
-        for (int k = 0; k < e->persist_grid; ++k)
-          std::fprintf(f, "%d %d %llu %llu\n", b, k, (unsigned long long)h[((size_t)b * e->persist_grid + k) * 2],
-                       (unsigned long long)h[((size_t)b * e->persist_grid + k) * 2 + 1]);
+      std::fprintf(f, "# token stage block t0 t1 t2 done (s_memrealtime ticks; 0 = not reached); %d stages per token, kinds:", e->prog_n);
+      std::vector<Stage> kinds(e->prog_n);
+      if (hipMemcpy(kinds.data(), e->prog[e->mode], sizeof(Stage) * e->prog_n, hipMemcpyDeviceToHost) == hipSuccess)
+        for (const Stage& k : kinds) std::fprintf(f, " %d", k.kind);
+      std::fprintf(f, "\n");
+      for (int k = 0; k < trace_tokens; ++k)
+        for (int i = 0; i < e->prog_n; ++i)
+          for (int b = 0; b < e->persist_grid; ++b) {
+            const uint64_t* q = &hbuf[(((size_t)k * e->prog_n + i) * e->persist_grid + b) * 4];
+            std::fprintf(f, "%d %d %d %llu %llu %llu %llu\n", k, i, b, (unsigned long long)q[0],
+                         (unsigned long long)q[1], (unsigned long long)q[2], (unsigned long long)q[3]);
+          }
       std::fclose(f);
     }
   }
   e->host_pos = out->pos;
   e->last_argmax = out->argmax;
-  if (out->err == 3) return QH_EDEVICE;
+  if (out->err == 3 || aborted != 0) return QH_EDEVICE;
   return QH_OK;
 }
 
@@ -408,8 +512,10 @@ int run_persist(qh_engine* e, int tok0, int n_prompt, int n_new, int eos, bool w
 int enqueue_step(qh_engine* e, bool with_logits, bool advance, hipStream_t s,
                  hipEvent_t head_t0 = nullptr, hipEvent_t head_t1 = nullptr) {
   std::vector<Stage> v;
-  build_layers(e, 0, kLayers, true, false, v);
-  v.push_back(head_stage(e, with_logits));
+  Bufs B;
+  Vec h{e->h, 0};
+  build_layers(e, 0, kLayers, true, B, v, h);
+  v.push_back(head_stage(e, B, h, with_logits, (int)v.size(), e->head_grid));
   QH_TRY(launch_stages(e, v, s, head_t0, head_t1));
   if (advance) QH_HIP(launch_advance(e->ctl, e->prompt_dev, e->out_dev, s));
   return QH_OK;
@@ -444,7 +550,8 @@ void release(qh_engine* e) {
         if (g) (void)hipGraphExecDestroy(g);
   void* bufs[] = {e->blob, e->rec, e->conv, e->kc, e->vc, e->h, e->convd, e->zb, e->gb, e->o, e->act,
                   e->og, e->qg, e->kraw, e->vraw, e->pm, e->pl, e->pacc, e->rope, e->logits, e->part_val,
-                  e->part_idx, e->ctl, e->prompt_dev, e->out_dev, e->prog[0], e->prog[1], e->bar};
+                  e->part_idx, e->ctl, e->prompt_dev, e->out_dev, e->prog[0], e->prog[1], e->arena,
+                  e->abort_dev};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -514,7 +621,7 @@ int create(const void* blob, size_t blob_len, const char* idx_text, int max_ctx,
   QH_C(dalloc(&e->logits, kVocab));
   QH_C(dalloc(&e->part_val, e->head_grid > 256 ? e->head_grid : 256));
   QH_C(dalloc(&e->part_idx, e->head_grid > 256 ? e->head_grid : 256));
-  QH_C(dalloc(&e->bar, kBarCounters * kBarStride + 64));
+  QH_C(dalloc(&e->abort_dev, 1));
   if (persist_max_grid(&e->persist_grid) != 0) e->persist_grid = 0;
   if (e->persist_grid == 0) e->exec = QH_EXEC_GRAPH;
   QH_C(dalloc(&e->ctl, 1));

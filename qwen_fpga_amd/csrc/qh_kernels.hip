@@ -8,8 +8,8 @@ namespace qh {
 
 template <int NCH, int MODE, int PRO, int R>
 __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
-  NoSync sync{a.done};
-  gemv_body<NCH, MODE, PRO, R>(a, blockIdx.x, gridDim.x, sync, a.tokv);
+  PlainIO io{a.done};
+  gemv_body<NCH, MODE, PRO, R>(a, blockIdx.x, gridDim.x, io, a.tokv);
 }
 
 template <int NCH, int MODE, int R>
@@ -50,7 +50,12 @@ hipError_t launch_gemv(const GemvArgs& a, int waves_per_block, hipStream_t s) {
   const int total = a.seg[a.nseg - 1].batch0 + a.seg[a.nseg - 1].nbatch;
   const int grid = (total + waves_per_block - 1) / waves_per_block;
   const dim3 blk(64 * waves_per_block);
+  if (a.rows_per_batch < 2)
+    for (int i = 0; i < a.nseg; ++i)
+      if (a.seg[i].epi == E_SWIGLU) return hipErrorInvalidValue;   // pair rows need R >= 2
   switch (a.rows_per_batch) {
+    case 1: return launch_gemv_r<1>(a, grid, blk, s);
+    case 2: return launch_gemv_r<2>(a, grid, blk, s);
     case 4: return launch_gemv_r<4>(a, grid, blk, s);
     case 8: return launch_gemv_r<8>(a, grid, blk, s);
     default: return hipErrorInvalidValue;
@@ -58,8 +63,8 @@ hipError_t launch_gemv(const GemvArgs& a, int waves_per_block, hipStream_t s) {
 }
 
 __global__ __launch_bounds__(256) void head_kernel(const HeadArgs a) {
-  NoSync sync{a.done};
-  head_body(a, blockIdx.x, gridDim.x, sync, a.logits);
+  PlainIO io{a.done};
+  head_body(a, blockIdx.x, gridDim.x, io, a.logits);
 }
 
 hipError_t launch_head(const HeadArgs& a, int grid, hipStream_t s) {
@@ -132,8 +137,8 @@ hipError_t launch_advance(StepCtl* ctl, const int* prompt, int* out_ids, hipStre
 }
 
 __global__ __launch_bounds__(256) void deltanet_kernel(const DnArgs a) {
-  NoSync sync{a.done};
-  deltanet_all(a, blockIdx.x, gridDim.x, sync, 0);
+  PlainIO io{a.done};
+  deltanet_all(a, blockIdx.x, gridDim.x, io, 0);
 }
 
 hipError_t launch_deltanet(const DnArgs& a, hipStream_t s) {
@@ -143,13 +148,13 @@ hipError_t launch_deltanet(const DnArgs& a, hipStream_t s) {
 }
 
 __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
-  NoSync sync{a.done};
-  attn_body(a, ldc_i(a.T), blockIdx.x, gridDim.x, sync);
+  PlainIO io{a.done};
+  attn_body(a, ldc_i(a.T), blockIdx.x, gridDim.x, io);
 }
 
 __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
-  NoSync sync{a.done};
-  combine_body(a, ldc_i(a.T), blockIdx.x, sync);
+  PlainIO io{a.done};
+  combine_body(a, ldc_i(a.T), blockIdx.x, io);
 }
 
 hipError_t launch_attn(const AttnArgs& a, hipStream_t s) {

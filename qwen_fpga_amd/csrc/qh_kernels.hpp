@@ -40,6 +40,8 @@ struct Seg {
   const float* sw2 = nullptr;
   float* out = nullptr;
   int32_t* acc_out = nullptr;
+  const float* res = nullptr;             // E_RESID: residual input (== out for in-place plain I/O)
+  int res_st = 0;                         // stage that produced res (tagged I/O)
   const float* c0 = nullptr;              // E_CONV: taps [C][4]   E_GATE_A: A_log
   const float* c1 = nullptr;              // E_GATE_A: dt_bias
   float* c2 = nullptr;                    // E_CONV: state [C][4]
@@ -60,6 +62,8 @@ struct GemvArgs {
   int tokv = 0;                 // the token id itself when tok is null
   float* h_out = nullptr;       // receives the embedded row (block 0)
   const int* done = nullptr;    // engine stop flag (skip when *done != 0)
+  int x_st = 0, z_st = 0;       // producer stages of x / z (tagged I/O)
+  int out_st = 0;               // this stage: tag of every output (segments and h_out)
   int nseg = 0;
   Seg seg[4];
 };
@@ -76,6 +80,7 @@ struct HeadArgs {
   float* part_val = nullptr;    // [grid] block maxima
   int* part_idx = nullptr;
   const int* done = nullptr;
+  int h_st = 0, part_st = 0;    // producer of h / this stage (tagged I/O)
 };
 
 // Decode-step control block, device resident.
@@ -113,6 +118,9 @@ struct AttnArgs {
   float* og = nullptr;           // combine output [2048]
   float eps = 1e-6f;
   const int* done = nullptr;
+  int qkv_st = 0;                // producer of qg / kraw / vraw (tagged I/O)
+  int part_st = 0;               // attention stage: pm / pl / pacc
+  int og_st = 0;                 // combine stage: og
 };
 
 struct DnArgs {
@@ -139,17 +147,20 @@ struct DnArgs {
   int normalize = 1;             // l2norm q,k and scale q (0: given already normalized)
   int heads = 16;                // heads to process (1 for the single-head op)
   const int* done = nullptr;
+  int convd_st = 0, gx_st = 0;   // producers of convd / gx (tagged I/O)
+  int o_st = 0;                  // this stage
 };
 
 struct Floats64 { float v[64]; };
 
-// One stage of the persistent decode kernel: the arguments a per-stage kernel
-// would get, and which body runs them.
+// One stage of a decode step: the arguments a per-stage kernel would get, and
+// which body runs them.  The three K > 1024 GEMVs use one row per wave batch
+// (1024 rows = 1024 batches), so every wave of a 256-workgroup grid streams.
 enum StageKind : int {
   ST_GEMV_NORM_1x8 = 0,    // gemv_body<1, mode, P_NORM, 8>   in_proj / q,k,v / gate,up
-  ST_GEMV_GATED_2x4 = 1,   // gemv_body<2, mode, P_GATED, 4>  DeltaNet out_proj
-  ST_GEMV_LOAD_2x4 = 2,    // gemv_body<2, mode, P_LOAD, 4>   attention o_proj
-  ST_GEMV_LOAD_4x4 = 3,    // gemv_body<4, mode, P_LOAD, 4>   MLP down
+  ST_GEMV_GATED_2x1 = 1,   // gemv_body<2, mode, P_GATED, 1>  DeltaNet out_proj
+  ST_GEMV_LOAD_2x1 = 2,    // gemv_body<2, mode, P_LOAD, 1>   attention o_proj
+  ST_GEMV_LOAD_4x1 = 3,    // gemv_body<4, mode, P_LOAD, 1>   MLP down
   ST_DELTANET = 4,
   ST_ATTN = 5,
   ST_COMBINE = 6,
@@ -164,24 +175,23 @@ struct Stage {
 };
 
 // Persistent decode: prog[0..nstage) is one token (embed .. LM head).  The
-// kernel runs tokens until the run_hls loop of StepCtl stops it.
+// kernel runs tokens until the run_hls loop of StepCtl stops it.  Workgroups
+// hand vectors to one another through tagged buffers (see TagIO): stage i of
+// the k-th token of the launch tags its outputs tag_base + k * kTagsPerToken + i.
+constexpr int kTagsPerToken = 256;
 struct PersistArgs {
   const Stage* prog = nullptr;
   int nstage = 0;
   int mode = M_W8A16;
+  uint32_t tag_base = 1;
   StepCtl* ctl = nullptr;       // in: tok, pos, step, n_prompt, n_new, n_out, eos, max_ctx; out: all
   const int* prompt = nullptr;  // [n_prompt]
   int* out_ids = nullptr;       // [n_new]
   float* logits = nullptr;      // optional: logits of every step (the last one remains)
-  float* part_val = nullptr;    // [grid] LM-head partial maxima
-  int* part_idx = nullptr;
-  unsigned* bar = nullptr;      // grid-barrier counters (zeroed before launch)
-  int* abort_flag = nullptr;    // set when a barrier wait exceeds its spin limit
-  uint64_t* trace = nullptr;    // optional [trace_bars][grid][2]: arrival / release time per barrier
-  int trace_bars = 0;
+  int* abort_flag = nullptr;    // set when a hand-over wait exceeds its poll limit
+  uint64_t* trace = nullptr;    // optional [trace_tokens][nstage][grid]: completion time of each stage
+  int trace_tokens = 0;
 };
-constexpr int kBarCounters = 16;      // arrival counters (workgroup b counts on b % 16)
-constexpr int kBarStride = 64;        // uints between counters (256 B)
 constexpr int kPersistThreads = 256;
 
 hipError_t launch_persist(const PersistArgs& a, int grid, hipStream_t s);

@@ -1,112 +1,74 @@
 // Persistent decode kernel: one cooperative launch runs whole tokens -- every
 // stage of every layer, the LM head, the argmax and the run_hls generation
-// bookkeeping (run_hls.cpp:56-66) -- with a grid barrier between dependent
-// stages instead of a kernel boundary.
+// bookkeeping (run_hls.cpp:56-66).  There is no grid barrier: workgroups hand
+// vectors to one another through tagged buffers (TagIO in qh_stages.hpp), so
+// each one waits only for the inputs of its own next work item.  A workgroup
+// that finishes a stage issues the next stage's weight (and own-state) loads
+// at once and then polls for that stage's inputs: HBM streaming overlaps the
+// hand-over latency.
 //
-// A workgroup arrives at the barrier as soon as its stores of stage k have
-// completed, then issues stage k+1's first weight (and own-state) loads, then
-// waits: HBM streaming and descriptor reads overlap the barrier latency.
-// Consumers read handed-over activations with device-coherent loads
-// (qh_device.hpp ldc*).
+// Every stage writes its own buffers (the engine gives each stage of the
+// token program distinct output vectors), so within a token no buffer is
+// written twice.  Across tokens, a stage rewrites its buffers only after the
+// argmax of the previous token, which every workgroup computes from the head
+// partials of all workgroups -- by then every workgroup has finished every
+// stage of the previous token, including its reads.
 #include "qh_stages.hpp"
 
 namespace qh {
 
-namespace {
-
-constexpr unsigned kSpinLimit = 1u << 21;   // ~1 s of polling: a barrier that never fills aborts
-
-struct GridBar {
-  unsigned* cnt;
-  int* abort_flag;
-  int blk, nblk;
-  unsigned gen;
-  int* s_stop;   // LDS: this workgroup saw an abort
-  uint64_t* trace;
-  unsigned trace_bars;
-
-  // All waves' stores have completed (each wave waits for its own), then one
-  // arrival per workgroup on counter blk % kBarCounters.
-  __device__ __forceinline__ void arrive() {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    ++gen;
-    if (threadIdx.x == 0) {
-      if (trace != nullptr && gen <= trace_bars)
-        trace[((size_t)(gen - 1) * nblk + blk) * 2] = __builtin_amdgcn_s_memrealtime();
-      __hip_atomic_fetch_add(cnt + (blk % kBarCounters) * kBarStride, 1u, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-
-  // Every counter has its workgroups of this generation; false after an abort.
-  __device__ __forceinline__ bool wait() {
-    const int t = threadIdx.x;
-    if (t < kBarCounters) {
-      const unsigned target = gen * (unsigned)(nblk / kBarCounters);
-      const unsigned* c = cnt + t * kBarStride;
-      unsigned spins = 0;
-      while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-        if ((++spins & 255u) == 0) {
-          if (spins > kSpinLimit) {
-            stc_i(abort_flag, 1);
-            *s_stop = 1;
-            break;
-          }
-          if (ldc_i(abort_flag) != 0) {
-            *s_stop = 1;
-            break;
-          }
-        }
-      }
-    }
-    __syncthreads();
-    if (trace != nullptr && t == 0 && gen <= trace_bars)
-      trace[((size_t)(gen - 1) * nblk + blk) * 2 + 1] = __builtin_amdgcn_s_memrealtime();
-    return *s_stop == 0;
-  }
-};
-
-}  // namespace
-
 template <int MODE>
 __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistArgs P) {
-  __shared__ int s_stop;
   __shared__ float s_bv[kPersistThreads / 64];
   __shared__ int s_bi[kPersistThreads / 64];
   const int blk = blockIdx.x, nblk = gridDim.x;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  if (t == 0) s_stop = 0;
-  __syncthreads();
-  GridBar bar{P.bar, P.abort_flag, blk, nblk, 0u, &s_stop, P.trace, (unsigned)P.trace_bars};
+  TagIO io;
+  io.abort_flag = P.abort_flag;
 
   // block-local copy of the generation state; every workgroup makes the same decisions
   int tok = P.ctl->tok, pos = P.ctl->pos, step = P.ctl->step, n_out = P.ctl->n_out;
   const int n_prompt = P.ctl->n_prompt, n_new = P.ctl->n_new, eos = P.ctl->eos, max_ctx = P.ctl->max_ctx;
-  int argmax = P.ctl->argmax, done = 0, err = 0;
+  int argmax = P.ctl->argmax, done = 0, err = 0, aborted = 0;
+  const HeadArgs& hd = P.prog[P.nstage - 1].hd;
 
-  while (true) {
+  for (int k = 0;; ++k) {
+    io.tag0 = P.tag_base + (uint32_t)k * (uint32_t)kTagsPerToken;
     for (int i = 0; i < P.nstage; ++i) {
       const Stage& st = P.prog[i];
+      uint64_t* tr = (P.trace != nullptr && k < P.trace_tokens) ? P.trace + (((size_t)k * P.nstage + i) * nblk + blk) * 4 : nullptr;
+      io.tr = tr;
+      bool ok;
       switch (st.kind) {
-        case ST_GEMV_NORM_1x8: gemv_body<1, MODE, P_NORM, 8>(st.g, blk, nblk, bar, tok); break;
-        case ST_GEMV_GATED_2x4: gemv_body<2, MODE, P_GATED, 4>(st.g, blk, nblk, bar, tok); break;
-        case ST_GEMV_LOAD_2x4: gemv_body<2, MODE, P_LOAD, 4>(st.g, blk, nblk, bar, tok); break;
-        case ST_GEMV_LOAD_4x4: gemv_body<4, MODE, P_LOAD, 4>(st.g, blk, nblk, bar, tok); break;
-        case ST_DELTANET: deltanet_all(st.d, blk, nblk, bar, tok); break;
-        case ST_ATTN: attn_body(st.at, pos, blk, nblk, bar); break;
-        case ST_COMBINE: combine_body(st.at, pos, blk, bar); break;
-        default: head_body(st.hd, blk, nblk, bar, P.logits); break;
+        case ST_GEMV_NORM_1x8: ok = gemv_body<1, MODE, P_NORM, 8>(st.g, blk, nblk, io, tok); break;
+        case ST_GEMV_GATED_2x1: ok = gemv_body<2, MODE, P_GATED, 1>(st.g, blk, nblk, io, tok); break;
+        case ST_GEMV_LOAD_2x1: ok = gemv_body<2, MODE, P_LOAD, 1>(st.g, blk, nblk, io, tok); break;
+        case ST_GEMV_LOAD_4x1: ok = gemv_body<4, MODE, P_LOAD, 1>(st.g, blk, nblk, io, tok); break;
+        case ST_DELTANET: ok = deltanet_all(st.d, blk, nblk, io, tok); break;
+        case ST_ATTN: ok = attn_body(st.at, pos, blk, nblk, io); break;
+        case ST_COMBINE: ok = combine_body(st.at, pos, blk, io); break;
+        default: ok = head_body(st.hd, blk, nblk, io, P.logits); break;
       }
-      if (s_stop) break;
+      if (tr != nullptr && t == 0) tr[3] = __builtin_amdgcn_s_memrealtime();
+      if (!ok) {
+        aborted = 1;
+        break;
+      }
     }
-    if (s_stop) break;
-    // argmax over the LM-head partials (qwen_synth.hpp:81-88), then ++pos (:90)
-    bar.arrive();
-    if (!bar.wait()) break;
+    if (aborted) break;
+    // argmax over the LM-head partials of all workgroups (qwen_synth.hpp:81-88), then ++pos (:90)
     float bv = -1e30f;
     int bi = 0;
-    for (int b = t; b < nblk; b += kPersistThreads) better(bv, bi, ldc(P.part_val + b), ldc_i(P.part_idx + b));
+    {
+      float* pv = io.slot();
+      float* pi = io.slot();
+      if (!io.stage_vec(hd.part_val, hd.part_st, nblk, pv) ||
+          !io.stage_vec(reinterpret_cast<const float*>(hd.part_idx), hd.part_st, nblk, pi)) {
+        aborted = 1;
+        break;
+      }
+      for (int b = t; b < nblk; b += kPersistThreads) better(bv, bi, pv[b], __float_as_int(pi[b]));
+    }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
       const float ov = __shfl_xor(bv, off, 64);
@@ -151,7 +113,7 @@ __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistA
     c->step = step;
     c->n_out = n_out;
     c->done = done;
-    c->err = s_stop ? 3 : err;
+    c->err = aborted ? 3 : err;
   }
 }
 
@@ -170,14 +132,14 @@ int persist_max_grid(int* grid) {
   occ = occ < occ2 ? occ : occ2;
   if (occ < 1) return -1;
   int g = ncu < 256 ? ncu : 256;   // one workgroup per CU
-  g -= g % kBarCounters;
-  if (g < kBarCounters) return -1;
+  g -= g & 1;                      // the head partials are copied as pairs
+  if (g < 2) return -1;
   *grid = g;
   return 0;
 }
 
 hipError_t launch_persist(const PersistArgs& a, int grid, hipStream_t s) {
-  if (grid < kBarCounters || grid % kBarCounters != 0) return hipErrorInvalidValue;
+  if (grid < 1 || grid > 256) return hipErrorInvalidValue;
   void* args[] = {const_cast<PersistArgs*>(&a)};
   const void* fn = a.mode == M_W8A8 ? reinterpret_cast<const void*>(persist_kernel<M_W8A8>)
                                     : reinterpret_cast<const void*>(persist_kernel<M_W8A16>);

@@ -2,40 +2,299 @@
 // (qh_kernels.hip: op-level C ABI and the graph engine) and the persistent
 // decode kernel (qh_persist.hip).  Each body runs as
 //
-//   sync.arrive()   this workgroup's earlier stores have completed; it
-//                   announces that to the others
+//   io.arrive()     (no-op hook kept for symmetry with the stage boundary)
 //   prefetch        weights / own state of the first work item in flight
-//   sync.wait()     every workgroup has arrived: inputs are visible
-//   compute         activations read with device-coherent loads (ldc*),
-//                   results stored with device-coherent stores (stc*)
+//   io.wait()       the per-stage kernels check the engine's stop flag here
+//   compute         vectors produced by other workgroups are read through the
+//                   I/O policy, results are written through it
 //
-// The per-stage kernels pass a Sync whose wait() only checks the engine's stop
-// flag; the persistent kernel passes its grid barrier.  Work items (row
-// batches, heads, attention splits) are assigned to (workgroup, wave) by the
-// same formulas in both, and every value is produced by the same code, so the
-// two paths are bit-identical.
+// Two I/O policies:
+//   PlainIO  fp32 vectors with device-coherent loads and stores (sc1).  The
+//            per-stage kernels use it: kernel boundaries order producers and
+//            consumers.
+//   TagIO    a vector element i is the 8-byte pair {value bits, tag} at byte
+//            8 i, written by one 64-bit store.  A consumer polls the pairs it
+//            needs until every tag equals the tag of the producing stage of
+//            the current token, so a consumer waits for exactly its inputs and
+//            there is no grid-wide barrier.  The persistent kernel uses it.
+//
+// Work items (row batches, heads, attention splits) are assigned to
+// (workgroup, wave) by the same formulas under both policies, and every value
+// is produced by the same code, so the two paths are bit-identical.
 #pragma once
 #include "qh_device.hpp"
 #include "qh_kernels.hpp"
 
 namespace qh {
 
-struct NoSync {
-  const int* done = nullptr;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+
+// A value loaded before it is needed (epilogue residual): raw bits and tag.
+struct Raw {
+  uint32_t v = 0, t = 0;
+};
+
+__device__ __forceinline__ bool wave_all(bool ok) { return __builtin_amdgcn_ballot_w64(!ok) == 0; }
+
+// Workgroup copies of handed-over vectors (GEMV inputs, the LM head's h): a
+// ring of four 4096-float slots.  A workgroup takes the slots in order, one or
+// two per stage, and each copy ends with a workgroup barrier, so a slot is
+// rewritten only after every wave has passed two later barriers -- long after
+// its last read of the slot's previous contents.
+constexpr int kLdsSlot = 4096;
+__device__ __forceinline__ float* lds_ring() {
+  __shared__ float ring[4 * kLdsSlot];
+  return ring;
+}
+
+struct PlainIO {
+  static constexpr bool kTagged = false;
+  const int* done = nullptr;   // engine stop flag (graph engine); null: never stopped
+  int ring = 0;                // next LDS slot
+  __device__ __forceinline__ float* slot() { return lds_ring() + kLdsSlot * (ring++ & 3); }
+  __device__ __forceinline__ void mark(int) {}
   __device__ __forceinline__ void arrive() {}
   __device__ __forceinline__ bool wait() { return done == nullptr || ldc_i(done) == 0; }
+  // N chunks of 16 consecutive elements starting at idx[j] (a multiple of 4)
+  template <int N>
+  __device__ __forceinline__ bool ld16(const float* base, int, const int (&idx)[N], float (&v)[N][16]) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) ldc16(base, idx[j], v[j]);
+    return true;
+  }
+  template <int N>
+  __device__ __forceinline__ bool ldn(const float* base, int, const int (&idx)[N], float (&v)[N]) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] = ldcb(base, idx[j]);
+    return true;
+  }
+  __device__ __forceinline__ bool ld1(const float* base, int, int idx, float& v) {
+    v = ldcb(base, idx);
+    return true;
+  }
+  __device__ __forceinline__ bool ld1i(const int* base, int, int idx, int& v) {
+    v = __float_as_int(ldcb(reinterpret_cast<const float*>(base), idx));
+    return true;
+  }
+  __device__ __forceinline__ Raw issue1(const float* base, int idx) {
+    Raw r;
+    r.v = __float_as_uint(ldcb(base, idx));
+    return r;
+  }
+  __device__ __forceinline__ bool resolve1(const Raw& r, const float*, int, int, float& v) {
+    v = __uint_as_float(r.v);
+    return true;
+  }
+  __device__ __forceinline__ void st1(float* base, int, int idx, float v) { stcb(base, idx, v); }
+  __device__ __forceinline__ void st1i(int* base, int, int idx, int v) {
+    stcb(reinterpret_cast<float*>(base), idx, __int_as_float(v));
+  }
+  __device__ __forceinline__ void st16(float* base, int, int idx, const float* v) { stc16(base, idx, v); }
+  // The whole workgroup copies elements [0, K) (K a multiple of 4) into lds;
+  // every thread must call it (it ends with a workgroup barrier).
+  __device__ __forceinline__ bool stage_vec(const float* base, int, int K, float* lds) {
+    for (int i = 4 * (int)threadIdx.x; i < K; i += 4 * (int)blockDim.x) {
+      float v[4];
+      ldc4(base, i, v);
+      *reinterpret_cast<float4*>(lds + i) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    __syncthreads();
+    return true;
+  }
+};
+
+// Polls before a hand-over wait gives up (one poll is a memory round trip,
+// roughly a microsecond): about a second, then the launch aborts.
+constexpr unsigned kPollLimit = 1u << 20;
+
+struct TagIO {
+  static constexpr bool kTagged = true;
+  uint32_t tag0 = 0;          // tag of stage 0 of the current token
+  int* abort_flag = nullptr;  // global: set by the first wave that gives up
+  int ring = 0;               // next LDS slot
+  __device__ __forceinline__ float* slot() { return lds_ring() + kLdsSlot * (ring++ & 3); }
+  uint64_t* tr = nullptr;     // optional timing trace of the current stage (points 0..2)
+  __device__ __forceinline__ void mark(int p) {
+    if (tr != nullptr && threadIdx.x == 0) tr[p] = __builtin_amdgcn_s_memrealtime();
+  }
+  __device__ __forceinline__ uint32_t tag(int st) const { return tag0 + (uint32_t)st; }
+  __device__ __forceinline__ void arrive() {}
+  __device__ __forceinline__ bool wait() { return true; }
+  // After a failed poll: false once the limit is reached or another wave gave up.
+  __device__ __forceinline__ bool again(unsigned& polls) {
+    ++polls;
+    if ((polls & 63u) == 0) {
+      if (polls > kPollLimit) {
+        stc_i(abort_flag, 1);
+        return false;
+      }
+      if (ldc_i(abort_flag) != 0) return false;
+    }
+    return true;
+  }
+  // Phase 1 of every wait: while the producers are still at work a wave polls
+  // one pair per lane (512 bytes), so waiting consumers put almost no load on
+  // the memory fabric that the producers' weight streams use.
+  __device__ __forceinline__ bool sample(const __amdgpu_buffer_rsrc_t& rs, int idx, uint32_t tg, unsigned& polls) {
+    while (true) {
+      asm volatile("" ::: "memory");
+      const u32x2 u = __builtin_amdgcn_raw_buffer_load_b64(rs, idx * 8, 0, kSc1);
+      if (wave_all(u[1] == tg)) return true;
+      if (!again(polls)) return false;
+    }
+  }
+  template <int N>
+  __device__ __forceinline__ bool ld16(const float* base, int st, const int (&idx)[N], float (&v)[N][16]) {
+    const uint32_t tg = tag(st);
+    const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
+    unsigned polls = 0;
+    for (bool first = true;; first = false) {
+      // after a miss, wait on one pair per lane before loading everything again
+      if (!first && !sample(rs, idx[N - 1] + 15, tg, polls)) return false;
+      asm volatile("" ::: "memory");   // re-issue the loads on every poll
+      u32x4 u[N][8];
+#pragma unroll
+      for (int j = 0; j < N; ++j)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) u[j][k] = __builtin_amdgcn_raw_buffer_load_b128(rs, (idx[j] + 2 * k) * 8, 0, kSc1);
+      bool ok = true;
+#pragma unroll
+      for (int j = 0; j < N; ++j)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) ok = ok & (u[j][k][1] == tg) & (u[j][k][3] == tg);
+      if (wave_all(ok)) {
+#pragma unroll
+        for (int j = 0; j < N; ++j)
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            v[j][2 * k] = __uint_as_float(u[j][k][0]);
+            v[j][2 * k + 1] = __uint_as_float(u[j][k][2]);
+          }
+        return true;
+      }
+      if (!again(polls)) return false;
+    }
+  }
+  template <int N>
+  __device__ __forceinline__ bool ldn(const float* base, int st, const int (&idx)[N], float (&v)[N]) {
+    const uint32_t tg = tag(st);
+    const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
+    unsigned polls = 0;
+    for (bool first = true;; first = false) {
+      if (N > 1 && !first && !sample(rs, idx[N - 1], tg, polls)) return false;
+      asm volatile("" ::: "memory");
+      u32x2 u[N];
+#pragma unroll
+      for (int j = 0; j < N; ++j) u[j] = __builtin_amdgcn_raw_buffer_load_b64(rs, idx[j] * 8, 0, kSc1);
+      bool ok = true;
+#pragma unroll
+      for (int j = 0; j < N; ++j) ok = ok & (u[j][1] == tg);
+      if (wave_all(ok)) {
+#pragma unroll
+        for (int j = 0; j < N; ++j) v[j] = __uint_as_float(u[j][0]);
+        return true;
+      }
+      if (!again(polls)) return false;
+    }
+  }
+  __device__ __forceinline__ bool ld1(const float* base, int st, int idx, float& v) {
+    int i1[1] = {idx};
+    float v1[1];
+    const bool ok = ldn<1>(base, st, i1, v1);
+    v = v1[0];
+    return ok;
+  }
+  __device__ __forceinline__ bool ld1i(const int* base, int st, int idx, int& v) {
+    float f;
+    const bool ok = ld1(reinterpret_cast<const float*>(base), st, idx, f);
+    v = __float_as_int(f);
+    return ok;
+  }
+  __device__ __forceinline__ Raw issue1(const float* base, int idx) {
+    const u32x2 u = __builtin_amdgcn_raw_buffer_load_b64(coh_rsrc(base), idx * 8, 0, kSc1);
+    Raw r;
+    r.v = u[0];
+    r.t = u[1];
+    return r;
+  }
+  __device__ __forceinline__ bool resolve1(const Raw& r, const float* base, int st, int idx, float& v) {
+    if (wave_all(r.t == tag(st))) {
+      v = __uint_as_float(r.v);
+      return true;
+    }
+    return ld1(base, st, idx, v);
+  }
+  __device__ __forceinline__ void st1(float* base, int st, int idx, float v) {
+    u32x2 u;
+    u[0] = __float_as_uint(v);
+    u[1] = tag(st);
+    __builtin_amdgcn_raw_buffer_store_b64(u, coh_rsrc(base), idx * 8, 0, kSc1);
+  }
+  __device__ __forceinline__ void st1i(int* base, int st, int idx, int v) {
+    st1(reinterpret_cast<float*>(base), st, idx, __int_as_float(v));
+  }
+  // The whole workgroup (kPersistThreads threads) copies elements [0, K) of a
+  // tagged vector into lds as fp32, K <= 4096 and even: every wave first polls
+  // 64 samples spread over the vector, then each thread loads its pairs (all
+  // loads in flight at once) until their tags match.  Ends with a barrier.
+  __device__ __forceinline__ bool stage_vec(const float* base, int st, int K, float* lds) {
+    constexpr int kL = 4096 / (2 * kPersistThreads);   // b128 loads per thread
+    const uint32_t tg = tag(st);
+    const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
+    const int t = threadIdx.x, lane = t & 63;
+    unsigned polls = 0;
+    for (bool first = true;; first = false) {
+      if (!first && !sample(rs, (int)(((unsigned)(2 * lane + 1) * (unsigned)K) >> 7), tg, polls)) return false;
+      asm volatile("" ::: "memory");
+      u32x4 u[kL];
+#pragma unroll
+      for (int i = 0; i < kL; ++i) {
+        const int p = min(2 * t + 2 * kPersistThreads * i, K - 2);
+        u[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, p * 8, 0, kSc1);
+      }
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < kL; ++i) ok = ok & (u[i][1] == tg) & (u[i][3] == tg);
+      if (wave_all(ok)) {
+#pragma unroll
+        for (int i = 0; i < kL; ++i) {
+          const int p = 2 * t + 2 * kPersistThreads * i;
+          if (p < K) *reinterpret_cast<float2*>(lds + p) = make_float2(__uint_as_float(u[i][0]), __uint_as_float(u[i][2]));
+        }
+        break;
+      }
+      if (!again(polls)) return false;
+    }
+    __syncthreads();
+    return true;
+  }
+  __device__ __forceinline__ void st16(float* base, int st, int idx, const float* v) {
+    const uint32_t tg = tag(st);
+    const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      u32x4 u;
+      u[0] = __float_as_uint(v[2 * k]);
+      u[1] = tg;
+      u[2] = __float_as_uint(v[2 * k + 1]);
+      u[3] = tg;
+      __builtin_amdgcn_raw_buffer_store_b128(u, rs, (idx + 2 * k) * 8, 0, kSc1);
+    }
+  }
 };
 
 // ===========================================================================
 // GEMV: y = W x over up to four row segments sharing one activation vector.
-// A wave owns batches of 8 rows; lane l holds the 16-element chunks
-// c = l + 64j of x in registers and streams the same chunks of each row with
-// one 16-byte load per chunk (a row of 1024 int8 is one coalesced 1 KiB read
-// across the wave).  After the lane partials, reduce8 folds the 8 rows with a
-// transposed xor butterfly: at offsets 32, 16, 8 each lane keeps half of its
-// rows and receives its partner's other half, then offsets 4, 2, 1 finish the
-// tree.  Lane l ends with row (l >> 3) & 7.  Per row this is exactly the
-// 64-lane xor tree of the C16 order.
+// A wave owns batches of R rows (R = 1, 2, 4 or 8); lane l holds the
+// 16-element chunks c = l + 64j of x in registers and streams the same chunks
+// of each row with one 16-byte load per chunk (a row of 1024 int8 is one
+// coalesced 1 KiB read across the wave).  After the lane partials, the R rows
+// are folded by a transposed xor butterfly: at offsets 32, 16, 8 each lane
+// keeps half of its rows and receives its partner's other half, then the
+// remaining offsets finish the tree.  Lane l ends with row (l >> (6 - log2 R))
+// & (R - 1).  Per row this is exactly the 64-lane xor tree of the C16 order,
+// whatever R is (IEEE addition is commutative).
 // ===========================================================================
 template <typename T>
 __device__ __forceinline__ T reduce8(T v[8], int lane) {
@@ -70,6 +329,69 @@ __device__ __forceinline__ T reduce8(T v[8], int lane) {
   return r;
 }
 
+template <typename T>
+__device__ __forceinline__ T reduce4(T v[4], int lane) {
+  {
+    const bool up = (lane & 32) != 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const T send = up ? v[i] : v[i + 2];
+      const T keep = up ? v[i + 2] : v[i];
+      v[i] = keep + __shfl_xor(send, 32, 64);
+    }
+  }
+  {
+    const bool up = (lane & 16) != 0;
+    const T send = up ? v[0] : v[1];
+    const T keep = up ? v[1] : v[0];
+    v[0] = keep + __shfl_xor(send, 16, 64);
+  }
+  T r = v[0];
+  r = r + __shfl_xor(r, 8, 64);
+  r = r + __shfl_xor(r, 4, 64);
+  r = r + __shfl_xor(r, 2, 64);
+  r = r + __shfl_xor(r, 1, 64);
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ T reduce2(T v[2], int lane) {
+  const bool up = (lane & 32) != 0;
+  const T send = up ? v[0] : v[1];
+  const T keep = up ? v[1] : v[0];
+  T r = keep + __shfl_xor(send, 32, 64);
+  r = r + __shfl_xor(r, 16, 64);
+  r = r + __shfl_xor(r, 8, 64);
+  r = r + __shfl_xor(r, 4, 64);
+  r = r + __shfl_xor(r, 2, 64);
+  r = r + __shfl_xor(r, 1, 64);
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ T reduce1(T v[1], int) {
+  T r = v[0];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) r = r + __shfl_xor(r, off, 64);
+  return r;
+}
+
+template <int R, typename T>
+__device__ __forceinline__ T reduce_rows(T v[R], int lane) {
+  if constexpr (R == 8)
+    return reduce8(v, lane);
+  else if constexpr (R == 4)
+    return reduce4(v, lane);
+  else if constexpr (R == 2)
+    return reduce2(v, lane);
+  else
+    return reduce1(v, lane);
+}
+template <int R>
+__device__ __forceinline__ int row_of_lane(int lane) {
+  return R == 1 ? 0 : (lane >> (R == 8 ? 3 : R == 4 ? 4 : 5)) & (R - 1);
+}
+
 __device__ __forceinline__ void load16f(const float* p, float* v) {
   const float4* q = reinterpret_cast<const float4*>(p);
 #pragma unroll
@@ -97,68 +419,25 @@ __device__ __forceinline__ float i8_at(const uint32_t* w, int e) {
   return (float)(int)(int8_t)(w[e >> 2] >> (8 * (e & 3)));
 }
 
-__device__ __forceinline__ const int8_t* seg_row(const Seg& g, int row, int K) {
-  if (g.kind == SEG_PAIR) return ((row & 1) ? g.w2 : g.w) + (size_t)(row >> 1) * K;
-  return g.w + (size_t)row * K;
-}
 __device__ __forceinline__ float seg_scale(const Seg& g, int row) {
   if (g.kind == SEG_PAIR) return (row & 1) ? g.sw2[row >> 1] : g.sw[row >> 1];
   return g.sw[row];
 }
 
-// Transposed xor-butterfly over R rows (R = 4 or 8): at offsets 32, 16 (, 8)
-// each lane keeps half of its rows and receives its partner's other half; the
-// remaining offsets finish the tree.  Lane l ends with row (l >> (6 - log2 R))
-// & (R - 1).  Per row this is the 64-lane xor tree of the C16 order.  Written
-// out per R so every index is static (no private array can end up in memory).
-template <typename T>
-__device__ __forceinline__ T reduce4(T v[4], int lane) {
-  {
-    const bool up = (lane & 32) != 0;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const T send = up ? v[i] : v[i + 2];
-      const T keep = up ? v[i + 2] : v[i];
-      v[i] = keep + __shfl_xor(send, 32, 64);
-    }
-  }
-  {
-    const bool up = (lane & 16) != 0;
-    const T send = up ? v[0] : v[1];
-    const T keep = up ? v[1] : v[0];
-    v[0] = keep + __shfl_xor(send, 16, 64);
-  }
-  T r = v[0];
-  r = r + __shfl_xor(r, 8, 64);
-  r = r + __shfl_xor(r, 4, 64);
-  r = r + __shfl_xor(r, 2, 64);
-  r = r + __shfl_xor(r, 1, 64);
-  return r;
-}
-template <int R, typename T>
-__device__ __forceinline__ T reduce_rows(T v[R], int lane) {
-  if constexpr (R == 8)
-    return reduce8(v, lane);
-  else
-    return reduce4(v, lane);
-}
-template <int R>
-__device__ __forceinline__ int row_of_lane(int lane) {
-  return R == 1 ? 0 : (lane >> (R == 8 ? 3 : R == 4 ? 4 : 5)) & (R - 1);
-}
-
-// Per-row epilogue inputs, loaded by the writer lanes at kernel start.
+// Per-row epilogue inputs, loaded by every lane for its row at batch start.
 struct EpiAux {
-  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;   // conv state cols 1..3 | residual | A_log
+  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;   // residual | conv state cols 1..3 | A_log
   float w0 = 0.0f, w1 = 0.0f, w2 = 0.0f, w3 = 0.0f;   // conv taps | dt_bias
   float sc = 1.0f;                                     // the row's weight scale (int8 segments)
+  Raw res;                                             // E_RESID: residual, resolved before use
 };
-__device__ __forceinline__ void epi_prefetch(const Seg& g, int myrow, EpiAux& x) {
+template <class IO>
+__device__ __forceinline__ void epi_prefetch(const Seg& g, int myrow, EpiAux& x, IO& io) {
   const int r = min(myrow, g.rows - 1);   // always a valid address; unused rows are never stored
   if (g.kind != SEG_F32) x.sc = seg_scale(g, r);
   switch (g.epi) {
     case E_RESID:
-      x.a0 = ldcb(g.out, r);   // residual: written by another workgroup
+      x.res = io.issue1(g.res, r);   // residual: written by another workgroup
       break;
     case E_GATE_A:
       x.a0 = g.c0[r];
@@ -182,35 +461,37 @@ __device__ __forceinline__ void epi_prefetch(const Seg& g, int myrow, EpiAux& x)
 }
 
 // Row-batch epilogue: the writer lane of each row stores its result y.
-template <int R>
-__device__ __forceinline__ void gemv_epilogue(const Seg& g, int lane, int myrow, float y, int acci,
-                                              const EpiAux& x) {
+template <int R, class IO>
+__device__ __forceinline__ void gemv_epilogue(const Seg& g, int ost, int lane, int myrow, float y, int acci,
+                                              const EpiAux& x, IO& io) {
   constexpr int LPR = 64 / R;   // lanes holding one row
-  if (g.epi == E_SWIGLU) {      // pair rows: even = gate i, odd = up i (mlp.hpp:17)
-    const float yo = __shfl_xor(y, LPR, 64);
-    if ((lane & (2 * LPR - 1)) == 0 && myrow < g.rows) stcb(g.out, myrow >> 1, dev_silu(y) * yo);
-    return;
+  if constexpr (R >= 2) {
+    if (g.epi == E_SWIGLU) {      // pair rows: even = gate i, odd = up i (mlp.hpp:17)
+      const float yo = __shfl_xor(y, LPR, 64);
+      if ((lane & (2 * LPR - 1)) == 0 && myrow < g.rows) io.st1(g.out, ost, myrow >> 1, dev_silu(y) * yo);
+      return;
+    }
   }
   if ((lane & (LPR - 1)) != 0 || myrow >= g.rows) return;
   switch (g.epi) {
     case E_STORE:
-      stcb(g.out, myrow, y);
+      io.st1(g.out, ost, myrow, y);
       break;
     case E_SILU:   // silu(z) for the gated norm (norm.hpp:32)
-      stcb(g.out, myrow, dev_silu(y));
+      io.st1(g.out, ost, myrow, dev_silu(y));
       break;
     case E_RESID:
-      stcb(g.out, myrow, x.a0 + y);
+      io.st1(g.out, ost, myrow, x.a0 + y);
       break;
     case E_ACC:
-      stcb(g.out, myrow, y);
+      io.st1(g.out, ost, myrow, y);
       g.acc_out[myrow] = acci;
       break;
     case E_GATE_B:
-      stcb(g.out, myrow, dev_sigmoid(y));
+      io.st1(g.out, ost, myrow, dev_sigmoid(y));
       break;
     case E_GATE_A:
-      stcb(g.out, myrow, -dev_expf(x.a0) * dev_softplus(y + x.w0));
+      io.st1(g.out, ost, myrow, -dev_expf(x.a0) * dev_softplus(y + x.w0));
       break;
     case E_CONV: {   // conv1d.hpp:22-36: window = state cols 1..3 + new sample
       float acc = 0.0f;
@@ -219,7 +500,7 @@ __device__ __forceinline__ void gemv_epilogue(const Seg& g, int lane, int myrow,
       acc = acc + x.a3 * x.w2;
       acc = acc + y * x.w3;
       *reinterpret_cast<float4*>(g.c2 + (size_t)myrow * 4) = make_float4(x.a1, x.a2, x.a3, y);
-      stcb(g.out, myrow, dev_silu(acc));
+      io.st1(g.out, ost, myrow, dev_silu(acc));
       break;
     }
     default:
@@ -258,8 +539,8 @@ __device__ __forceinline__ int seg_of(const GemvArgs& a, int b) {
   return __builtin_amdgcn_readfirstlane(si);
 }
 
-template <int NCH, int MODE, int PRO, int R, class Sync>
-__device__ __forceinline__ void gemv_body(const GemvArgs& a, int blk, int nblk, Sync& sync, int tokv) {
+template <int NCH, int MODE, int PRO, int R, class IO>
+__device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, IO& io, int tokv) {
   const int lane = threadIdx.x & 63, nwv = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int K = a.K, nchunk = K >> 4;
@@ -267,7 +548,9 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int blk, int nblk, 
   const int stride = nblk * nwv;
   int b = blk * nwv + wave;
 
-  sync.arrive();
+  io.arrive();
+  io.mark(0);
+  if (blk * nwv >= total) return true;   // no rows for this workgroup (workgroup-uniform)
   // ---------------- 1. weights and epilogue inputs of the first batch in flight first
   uint32_t w[NCH][R][4];
   EpiAux aux;
@@ -277,9 +560,32 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int blk, int nblk, 
     const Seg& g = a.seg[si];
     const int row0 = (b - g.batch0) * R;
     if (g.kind != SEG_F32) load_batch<NCH, R>(g, row0, K, nchunk, lane, w);
-    epi_prefetch(g, row0 + row_of_lane<R>(lane), aux);
+    epi_prefetch(g, row0 + row_of_lane<R>(lane), aux, io);
   }
-  if (!sync.wait()) return;
+  float nwv16[NCH][16];   // norm gains: constants, loaded before the hand-over wait
+  if constexpr (PRO == P_NORM || PRO == P_GATED) {
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = min(lane + 64 * j, nchunk - 1);
+      load16f(a.nw + (PRO == P_GATED ? ((16 * c) & 127) : 16 * c), nwv16[j]);
+    }
+  }
+  if (!io.wait()) return false;
+  // the workgroup's copy of x (and z): every wave takes part, rows or not
+  const float* xl = nullptr;
+  const float* zl = nullptr;
+  if (PRO != P_LOADQ && !(PRO == P_NORM && a.emb != nullptr)) {
+    float* buf = io.slot();
+    if (!io.stage_vec(a.x, a.x_st, K, buf)) return false;
+    xl = buf;
+  }
+  if constexpr (PRO == P_GATED) {
+    float* buf = io.slot();
+    if (!io.stage_vec(a.z, a.z_st, K, buf)) return false;
+    zl = buf;
+  }
+  io.mark(1);
+  if (b >= total) return true;   // no rows for this wave (block 0 / wave 0 always has some)
 
   // ---------------- 2. prologue: this lane's chunks c = lane + 64 j of x
   float xv[NCH][16];     // fp32 activation (W8A16) / dequantized q*s (W8A8)
@@ -296,14 +602,6 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int blk, int nblk, 
       for (int e = 0; e < 16; ++e) xv[j][e] = i8_at(xq[j], e) * xs;
     }
   } else {
-    float nwv16[NCH][16];
-    if constexpr (PRO == P_NORM || PRO == P_GATED) {
-#pragma unroll
-      for (int j = 0; j < NCH; ++j) {
-        const int c = min(lane + 64 * j, nchunk - 1);
-        load16f(a.nw + (PRO == P_GATED ? ((16 * c) & 127) : 16 * c), nwv16[j]);
-      }
-    }
     if (PRO == P_NORM && a.emb != nullptr) {   // embed_row (gemv.hpp:76-84)
       const int tok = a.tok != nullptr ? ldc_i(a.tok) : tokv;
       const int8_t* er = a.emb + (size_t)tok * K;
@@ -316,7 +614,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int blk, int nblk, 
           load16b(er + 16 * c, t);
 #pragma unroll
           for (int e = 0; e < 16; ++e) xv[j][e] = i8_at(t, e) * es;
-          if (a.h_out != nullptr && blk == 0 && threadIdx.x < 64) stc16(a.h_out, 16 * c, xv[j]);
+          if (a.h_out != nullptr && blk == 0 && threadIdx.x < 64) io.st16(a.h_out, a.out_st, 16 * c, xv[j]);
         } else {
 #pragma unroll
           for (int e = 0; e < 16; ++e) xv[j][e] = 0.0f;
@@ -325,9 +623,8 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int blk, int nblk, 
     } else {
 #pragma unroll
       for (int j = 0; j < NCH; ++j) {
-        const int c = lane + 64 * j;
-        ldc16(a.x, 16 * min(c, nchunk - 1), xv[j]);
-        if (c >= nchunk)
+        load16f(xl + 16 * min(lane + 64 * j, nchunk - 1), xv[j]);
+        if (lane + 64 * j >= nchunk)
 #pragma unroll
           for (int e = 0; e < 16; ++e) xv[j][e] = 0.0f;
       }
@@ -347,7 +644,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int blk, int nblk, 
     } else if constexpr (PRO == P_GATED) {   // heads of 128 = groups of 8 lanes; z holds silu(z)
       float zs[NCH][16];
 #pragma unroll
-      for (int j = 0; j < NCH; ++j) ldc16(a.z, 16 * (lane + 64 * j), zs[j]);
+      for (int j = 0; j < NCH; ++j) load16f(zl + 16 * (lane + 64 * j), zs[j]);
 #pragma unroll
       for (int j = 0; j < NCH; ++j) {
         float ss = dot16_f32(xv[j], xv[j], 0.0f);
@@ -431,7 +728,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int blk, int nblk, 
       const Seg& gn = a.seg[sin];
       const int rn = (bn - gn.batch0) * R;
       if (gn.kind != SEG_F32) load_batch<NCH, R>(gn, rn, K, nchunk, lane, w);
-      epi_prefetch(gn, rn + row_of_lane<R>(lane), auxn);
+      epi_prefetch(gn, rn + row_of_lane<R>(lane), auxn, io);
     }
     if (g.kind == SEG_F32 || MODE == M_W8A16) {
       y = reduce_rows<R>(pf, lane);
@@ -440,16 +737,20 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int blk, int nblk, 
       acci = reduce_rows<R>(pi, lane);
       y = ((float)acci * xs) * aux.sc;   // float(acc)*sx*sw
     }
-    gemv_epilogue<R>(g, lane, myrow, y, acci, aux);
+    if (g.epi == E_RESID && !io.resolve1(aux.res, g.res, g.res_st, min(myrow, g.rows - 1), aux.a0)) return false;
+    gemv_epilogue<R>(g, a.out_st, lane, myrow, y, acci, aux, io);
     si = sin;
     aux = auxn;
   }
+  io.mark(2);
+  return true;
 }
 
 // ===========================================================================
 // Tied LM head: final rmsnorm prologue, logits = (E row . h) * s in C16
 // order, running argmax with the reference's rule (strict >, so the first
-// index wins a tie; qwen_synth.hpp:81-88) folded per workgroup.
+// index wins a tie; qwen_synth.hpp:81-88) folded per workgroup.  Two batches
+// of 8 rows (16 KiB per wave) are in flight while a third is reduced.
 // ===========================================================================
 __device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
   if (v > bv || (v == bv && i < bi)) {
@@ -458,25 +759,34 @@ __device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
   }
 }
 
-template <class Sync>
-__device__ __forceinline__ void head_body(const HeadArgs& a, int blk, int nblk, Sync& sync, float* logits) {
+__device__ __forceinline__ void head_load(const HeadArgs& a, int b, int lane, int rl, uint32_t (&w)[8][4], float& sc) {
+#pragma unroll
+  for (int r = 0; r < 8; ++r) load16b(a.w + (size_t)(b * 8 + r) * 1024 + 16 * lane, w[r]);
+  sc = a.sw[b * 8 + rl];
+}
+
+template <class IO>
+__device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, IO& io, float* logits) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwv = blockDim.x >> 6;
   const int total = a.rows / kRowsPerBatch;
   const int stride = nblk * nwv;
   int b = blk * nwv + wave;
   const int rl = (lane >> 3) & 7;
-  sync.arrive();
-  uint32_t w[8][4];
-  float sc = 0.0f;
-  if (b < total) {   // first batch in flight before the norm prologue
-#pragma unroll
-    for (int r = 0; r < 8; ++r) load16b(a.w + (size_t)(b * 8 + r) * 1024 + 16 * lane, w[r]);
-    sc = a.sw[b * 8 + rl];
-  }
-  if (!sync.wait()) return;
+  io.arrive();
+  uint32_t w0[8][4], w1[8][4];
+  float sc0 = 0.0f, sc1 = 0.0f;
+  if (b < total) head_load(a, b, lane, rl, w0, sc0);   // two batches in flight before the norm prologue
+  if (b + stride < total) head_load(a, b + stride, lane, rl, w1, sc1);
   float xv[16], nw[16];
-  ldc16(a.h, 16 * lane, xv);
   load16f(a.nw + 16 * lane, nw);
+  io.mark(0);
+  if (!io.wait()) return false;
+  {
+    float* hl = io.slot();
+    if (!io.stage_vec(a.h, a.h_st, 1024, hl)) return false;
+    load16f(hl + 16 * lane, xv);
+  }
+  io.mark(1);
   float ss = dot16_f32(xv, xv, 0.0f);
   ss = xor_sum<64>(ss);
   const float inv = 1.0f / sqrtf(ss / 1024.0f + a.eps);
@@ -484,24 +794,37 @@ __device__ __forceinline__ void head_body(const HeadArgs& a, int blk, int nblk, 
   for (int e = 0; e < 16; ++e) xv[e] = (xv[e] * inv) * (1.0f + nw[e]);
   float bv = -1e30f;
   int bi = 0;
-  for (; b < total; b += stride) {
-    float p[8];
+  for (; b < total; b += 2 * stride) {
+    {   // batch b (w0); its slot is refilled with batch b + 2 stride before the reduction
+      float p[8];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) p[r] = dot16_i8f(w[r], xv, 0.0f);
-    const float scur = sc;
-    const int bn = b + stride;
-    if (bn < total) {   // next batch in flight during the reduction
-#pragma unroll
-      for (int r = 0; r < 8; ++r) load16b(a.w + (size_t)(bn * 8 + r) * 1024 + 16 * lane, w[r]);
-      sc = a.sw[bn * 8 + rl];
+      for (int r = 0; r < 8; ++r) p[r] = dot16_i8f(w0[r], xv, 0.0f);
+      const float scur = sc0;
+      if (b + 2 * stride < total) head_load(a, b + 2 * stride, lane, rl, w0, sc0);
+      const float y = reduce8(p, lane) * scur;
+      const int row = b * 8 + rl;
+      if ((lane & 7) == 0) {
+        if (logits != nullptr) logits[row] = y;
+        better(bv, bi, y, row);
+      }
     }
-    const float y = reduce8(p, lane) * scur;
-    const int row = b * 8 + rl;
-    if ((lane & 7) == 0) {
-      if (logits != nullptr) logits[row] = y;
-      better(bv, bi, y, row);
+    const int b1 = b + stride;
+    if (b1 >= total) break;
+    {   // batch b + stride (w1)
+      float p[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) p[r] = dot16_i8f(w1[r], xv, 0.0f);
+      const float scur = sc1;
+      if (b1 + 2 * stride < total) head_load(a, b1 + 2 * stride, lane, rl, w1, sc1);
+      const float y = reduce8(p, lane) * scur;
+      const int row = b1 * 8 + rl;
+      if ((lane & 7) == 0) {
+        if (logits != nullptr) logits[row] = y;
+        better(bv, bi, y, row);
+      }
     }
   }
+  io.mark(2);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     const float ov = __shfl_xor(bv, off, 64);
@@ -517,10 +840,14 @@ __device__ __forceinline__ void head_body(const HeadArgs& a, int blk, int nblk, 
   __syncthreads();
   if (threadIdx.x == 0) {
     for (int w2 = 1; w2 < nwv; ++w2) better(bv, bi, sv[w2], sx[w2]);
-    stc(a.part_val + blk, bv);
-    stc_i(a.part_idx + blk, bi);
+    // Every earlier store of this workgroup (cache rows, state) completes before
+    // the partial that the next token waits for is published.
+    if constexpr (IO::kTagged) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    io.st1(a.part_val, a.part_st, blk, bv);
+    io.st1i(a.part_idx, a.part_st, blk, bi);
   }
   __syncthreads();
+  return true;
 }
 
 // ===========================================================================
@@ -536,7 +863,8 @@ __device__ __forceinline__ void head_body(const HeadArgs& a, int blk, int nblk, 
 // Head h's gate projections from the layer input (see DnArgs), on one wave;
 // lane 0 returns (g, beta).  Same operations as the in_proj prologue and its
 // fp32 segments, so the values are bit-identical to computing them there.
-__device__ __forceinline__ void deltanet_gates(const DnArgs& a, int h, int tokv, float& g, float& beta) {
+template <class IO>
+__device__ __forceinline__ bool deltanet_gates(const DnArgs& a, int h, int tokv, float& g, float& beta, IO& io) {
   const int lane = threadIdx.x & 63;
   float xv[16];
   if (a.emb != nullptr) {   // embed_row (gemv.hpp:76-84)
@@ -547,7 +875,11 @@ __device__ __forceinline__ void deltanet_gates(const DnArgs& a, int h, int tokv,
 #pragma unroll
     for (int e = 0; e < 16; ++e) xv[e] = i8_at(t4, e) * es;
   } else {
-    ldc16(a.gx, 16 * lane, xv);
+    int idx[1] = {16 * lane};
+    float t1[1][16];
+    if (!io.template ld16<1>(a.gx, a.gx_st, idx, t1)) return false;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) xv[e] = t1[0][e];
   }
   if (a.gx_norm != nullptr) {   // norm.hpp:13-20
     float nw[16];
@@ -575,49 +907,58 @@ __device__ __forceinline__ void deltanet_gates(const DnArgs& a, int h, int tokv,
   const float ya = xor_sum<64>(dot16_f32(w, xv, 0.0f));
   beta = dev_sigmoid(yb);
   g = -dev_expf(a.A_log[h]) * dev_softplus(ya + a.dt_bias[h]);
+  return true;
 }
 
-template <class Sync>
-__device__ __forceinline__ void deltanet_body(const DnArgs& a, int unit, bool valid, Sync& sync, int tokv) {
+template <class IO>
+__device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool valid, IO& io, int tokv) {
   const int h = unit / kDnVQuarters, vq = unit % kDnVQuarters;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int vl = t & 31, kg = t >> 5, v = vq * 32 + vl;
   float* Sh = a.S + (size_t)h * 128 * 128;
   __shared__ float gbs[2];
-  sync.arrive();
+  io.arrive();
   float s[16];
+  bool ok = true;
   if (valid) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) s[i] = Sh[(kg * 16 + i) * 128 + v];   // state tile in flight first
     if (a.wa != nullptr && wave == 0) {   // inputs final before in_proj: off the critical path
-      float g0, b0;
-      deltanet_gates(a, h, tokv, g0, b0);
+      float g0 = 0.0f, b0 = 0.0f;
+      ok = deltanet_gates(a, h, tokv, g0, b0, io);
       if (lane == 0) {
         gbs[0] = g0;
         gbs[1] = b0;
       }
     }
   }
-  if (!sync.wait() || !valid) return;
+  io.mark(0);
+  if (!ok) return false;
+  if (!io.wait()) return false;
+  if (!valid) return true;
   __shared__ float qs[128], ks[128];
   __shared__ float part[8][32];
   __shared__ float dl[32];
   float g = 0.0f, beta = 0.0f;
-  if (a.wa == nullptr) {
-    g = ldcb(a.gb, h);
-    beta = ldcb(a.gb, 16 + h);
+  if constexpr (!IO::kTagged) {   // gates given by the op-level caller
+    if (a.wa == nullptr) {
+      g = ldcb(a.gb, h);
+      beta = ldcb(a.gb, 16 + h);
+    }
   }
-  const float vv = ldcb(a.convd, 4096 + h * 128 + v);
+  float vv;
+  if (!io.ld1(a.convd, a.convd_st, 4096 + h * 128 + v, vv)) return false;
   if (wave < 2) {   // wave 0: q, wave 1: k; lanes 0..7 hold 16 elements each
     const int src = (wave == 0 ? 0 : 2048) + h * 128;
     float x[16];
     float ss = 0.0f;
-    if (lane < 8) {
-      ldc16(a.convd, src + 16 * lane, x);
-      ss = dot16_f32(x, x, 0.0f);
-    } else {
+    {   // every lane polls (lanes >= 8 re-read lane 7's chunk and drop it)
+      int idx[1] = {src + 16 * min(lane, 7)};
+      float t1[1][16];
+      if (!io.template ld16<1>(a.convd, a.convd_st, idx, t1)) return false;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) x[e] = 0.0f;
+      for (int e = 0; e < 16; ++e) x[e] = lane < 8 ? t1[0][e] : 0.0f;
+      if (lane < 8) ss = dot16_f32(x, x, 0.0f);
     }
     if (a.normalize) {
       ss = xor_sum<8>(ss);
@@ -633,6 +974,7 @@ __device__ __forceinline__ void deltanet_body(const DnArgs& a, int unit, bool va
     if (lane < 8) store16f((wave == 0 ? qs : ks) + 16 * lane, x);
   }
   __syncthreads();
+  io.mark(1);
   if (a.wa != nullptr) {
     g = gbs[0];
     beta = gbs[1];
@@ -677,34 +1019,78 @@ __device__ __forceinline__ void deltanet_body(const DnArgs& a, int unit, bool va
     for (int off = 4; off >= 1; off >>= 1)
 #pragma unroll
       for (int gi = 0; gi < off; ++gi) pp[gi] = pp[gi] + pp[gi + off];
-    stcb(a.o, h * 128 + v, pp[0]);
+    io.st1(a.o, a.o_st, h * 128 + v, pp[0]);
   }
+  io.mark(2);
   __syncthreads();
+  return true;
 }
 
 // All heads * kDnVQuarters units; the first one of each workgroup prefetches.
-template <class Sync>
-__device__ __forceinline__ void deltanet_all(const DnArgs& a, int blk, int nblk, Sync& sync, int tokv) {
+template <class IO>
+__device__ __forceinline__ bool deltanet_all(const DnArgs& a, int blk, int nblk, IO& io, int tokv) {
   const int units = a.heads * kDnVQuarters;
-  deltanet_body(a, blk, blk < units, sync, tokv);
-  NoSync none;
-  for (int u = blk + nblk; u < units; u += nblk) deltanet_body(a, u, true, none, tokv);
+  if (!deltanet_body(a, blk, blk < units, io, tokv)) return false;
+  for (int u = blk + nblk; u < units; u += nblk)
+    if (!deltanet_body(a, u, true, io, tokv)) return false;
+  return true;
 }
 
 // ===========================================================================
 // Gated GQA attention, split-K flash decoding (attention.hpp:25-95).
 // Unit u = 2 s + j covers positions [64 s, 64 s + 64) of kv head j for the
-// four query heads 4j..4j+3 (GQA kv = h/4).  Each wave normalises and rotates
-// the four queries (QK-norm with (1+w), RoPE on dims 0..63) in the C16 layout:
-// 16 lanes x 16 dims, four positions per wave iteration.  The unit owning
-// slot T first writes the new K (normed, rotated) and V rows.  Scores are C16
-// dots scaled by 1/16; per head the split max m, p = exp(s - m), the 64-lane
-// tree sum l and the position-ordered fma sum acc = sum p v are written for
-// the combine step.  A given (s, j) always runs on the same workgroup, so the
-// cache rows it reads are the ones it wrote.
+// four query heads 4j..4j+3 (GQA kv = h/4).  Before its inputs are ready a unit
+// loads every cached K and V row of its split (positions < T): K in the C16
+// layout (16 lanes x 16 dims, four positions per wave iteration), V as one
+// dimension per thread.  Each wave then normalises and rotates the four
+// queries (QK-norm with (1+w), RoPE on dims 0..63); the unit whose split holds
+// slot T normalises and rotates the new K row itself, takes the new V row, and
+// writes both to the cache.  Scores are C16 dots scaled by 1/16; per head the
+// split max m, p = exp(s - m), the 64-lane tree sum l and the position-ordered
+// fma sum acc = sum p v are written for the combine step.  A split's cache rows
+// are written and read by the same unit.
 // ===========================================================================
-__device__ __forceinline__ void qk_norm_rope(float* x, const float* nw16, float eps, int g16,
-                                             const float* cs, const float* sn) {
+// Everything a unit can load before its inputs are ready: the cached K rows of
+// split s (positions < T) in the C16 layout, the q/k norm gains and this
+// position's RoPE row in registers; the cached V rows go straight to LDS
+// (global_load_lds_dwordx4, no registers), row i of the split at vl + 256 i.
+struct AttnPre {
+  float kreg[4][16];
+  float qn[16], kn[16], cs[16], sn[16];
+};
+__device__ __forceinline__ float* attn_vlds() {
+  __shared__ float vl[kAttnSplit * 256];
+  return vl;
+}
+__device__ __forceinline__ void attn_prefetch(const AttnArgs& a, int s, int j, int T, int rrow, AttnPre& pf) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int g16 = lane & 15, pg = lane >> 4;
+  const int t0 = s * kAttnSplit;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int tp = t0 + 16 * wave + 4 * it + pg;
+    if (tp < T) {
+      ldc16(a.kc, tp * 512 + j * 256 + 16 * g16, pf.kreg[it]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) pf.kreg[it][e] = 0.0f;
+    }
+  }
+  float* vl = attn_vlds();
+  const int nv = min(kAttnSplit, T - t0);   // rows before slot T (workgroup-uniform)
+  for (int i = wave; i < nv; i += 4)
+    __builtin_amdgcn_global_load_lds(static_cast<const void*>(a.vc + (size_t)(t0 + i) * 512 + j * 256 + 4 * lane),
+                                     (__attribute__((address_space(3))) void*)(vl + 256 * i), 16, 0, kSc1);
+  load16f(a.qn + 16 * g16, pf.qn);
+  load16f(a.kn + 16 * g16, pf.kn);
+  // rope.hpp:30-41 touches dims 0..63: lane g16 < 4 uses cos/sin[(16 g16 + e) & 31]
+  const float* cs = a.rope + (size_t)rrow * 64 + 16 * (g16 & 1);
+  load16f(cs, pf.cs);
+  load16f(cs + 32, pf.sn);
+}
+
+__device__ __forceinline__ void qk_norm_rope(float* x, const float* nw16, float eps, int g16, const float* cs16,
+                                             const float* sn16) {
   float ss = dot16_f32(x, x, 0.0f);
   ss = xor_sum<16>(ss);
   const float inv = 1.0f / sqrtf(ss / 256.0f + eps);
@@ -717,65 +1103,52 @@ __device__ __forceinline__ void qk_norm_rope(float* x, const float* nw16, float 
   if (g16 < 4) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int i = 16 * g16 + e;
-      const float half = (i < 32) ? -part[e] : part[e];
-      x[e] = x[e] * cs[i & 31] + half * sn[i & 31];
+      const float half = (g16 < 2) ? -part[e] : part[e];   // dims 0..31 take -x[i+32]
+      x[e] = x[e] * cs16[e] + half * sn16[e];
     }
   }
 }
 
-// cached K rows (positions < T) of this wave's 16 positions of split s
-__device__ __forceinline__ void attn_load_k(const AttnArgs& a, int s, int j, int T, float (&kreg)[4][16]) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g16 = lane & 15, pg = lane >> 4;
-  const int t0 = s * kAttnSplit;
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int tp = t0 + 16 * wave + 4 * it + pg;
-    if (tp < T) {
-      load16f(a.kc + (size_t)tp * 512 + j * 256 + 16 * g16, kreg[it]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) kreg[it][e] = 0.0f;
-    }
-  }
-}
-
-__device__ __forceinline__ void attn_unit(const AttnArgs& a, int s, int j, int T, float (&kreg)[4][16]) {
+template <class IO>
+__device__ __forceinline__ bool attn_unit(const AttnArgs& a, int s, int j, int T, AttnPre& pf, IO& io) {
   const int Tn = T + 1;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int g16 = lane & 15, pg = lane >> 4;
-  const int rrow = a.rope_row != nullptr ? ldc_i(a.rope_row) : T;
-  const float* cs = a.rope + (size_t)rrow * 64;
-  const float* sn = cs + 32;
   __shared__ float sc[4][64];
   __shared__ float pp[4][64];
+  const float* vl = attn_vlds();
   const int t0 = s * kAttnSplit;
   float q[4][16];
+  {
+    int idx[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int h = 4 * j + i;
-    ldc16(a.qg, h * 512 + 16 * g16, q[i]);   // query half of head h (attention.hpp:40)
-    float w[16];
-    load16f(a.qn + 16 * g16, w);
-    qk_norm_rope(q[i], w, a.eps, g16, cs, sn);
+    for (int i = 0; i < 4; ++i) idx[i] = (4 * j + i) * 512 + 16 * g16;   // query half of head 4j+i (attention.hpp:40)
+    io.mark(0);
+    if (!io.template ld16<4>(a.qg, a.qkv_st, idx, q)) return false;
+    io.mark(1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qk_norm_rope(q[i], pf.qn, a.eps, g16, pf.cs, pf.sn);
   }
-  if (T / kAttnSplit == s) {   // owner of slot T (attention.hpp:46-54)
-    if (wave == 0) {
-      float k[16], w[16], v[16];
-      ldc16(a.kraw, j * 256 + 16 * g16, k);
-      load16f(a.kn + 16 * g16, w);
-      qk_norm_rope(k, w, a.eps, g16, cs, sn);
-      ldc16(a.vraw, j * 256 + 16 * g16, v);
-      if (pg == 0) {
-        store16f(a.kc + (size_t)T * 512 + j * 256 + 16 * g16, k);
-        store16f(a.vc + (size_t)T * 512 + j * 256 + 16 * g16, v);
-      }
-    }
-    __syncthreads();
+  float vT = 0.0f;
+  if (T / kAttnSplit == s) {   // slot T lies in this split (attention.hpp:45-54)
+    float k[16];
+    {
+      int idx[1] = {j * 256 + 16 * g16};
+      float t1[1][16];
+      if (!io.template ld16<1>(a.kraw, a.qkv_st, idx, t1)) return false;
 #pragma unroll
-    for (int it = 0; it < 4; ++it)
-      if (t0 + 16 * wave + 4 * it + pg == T) load16f(a.kc + (size_t)T * 512 + j * 256 + 16 * g16, kreg[it]);
+      for (int e = 0; e < 16; ++e) k[e] = t1[0][e];
+      qk_norm_rope(k, pf.kn, a.eps, g16, pf.cs, pf.sn);
+    }
+    if (!io.ld1(a.vraw, a.qkv_st, j * 256 + t, vT)) return false;
+    if (wave == 0 && pg == 0) stc16(a.kc, T * 512 + j * 256 + 16 * g16, k);
+    stcb(a.vc, T * 512 + j * 256 + t, vT);
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const bool sel = t0 + 16 * wave + 4 * it + pg == T;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) pf.kreg[it][e] = sel ? k[e] : pf.kreg[it][e];
+    }
   }
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
@@ -783,11 +1156,12 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int s, int j, int T
     const bool valid = t0 + tl < Tn;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float d = dot16_f32(q[i], kreg[it], 0.0f);
+      float d = dot16_f32(q[i], pf.kreg[it], 0.0f);
       d = xor_sum<16>(d);
       if (g16 == 0) sc[i][tl] = valid ? d * 0.0625f : -__builtin_inff();
     }
   }
+  io.mark(2);
   __syncthreads();
   {
     const int i = wave;
@@ -798,75 +1172,96 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int s, int j, int T
     const float l = xor_sum<64>(p);
     pp[i][lane] = p;
     if (lane == 0) {
-      stcb(a.pm, (4 * j + i) * a.nsplit_max + s, m);
-      stcb(a.pl, (4 * j + i) * a.nsplit_max + s, l);
+      io.st1(a.pm, a.part_st, (4 * j + i) * a.nsplit_max + s, m);
+      io.st1(a.pl, a.part_st, (4 * j + i) * a.nsplit_max + s, l);
     }
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's V rows have reached LDS
   __syncthreads();
-  {
-    const int i = wave;
+  {   // thread t = dimension; position order (attention.hpp:80-86)
     const int cnt = min(kAttnSplit, Tn - t0);
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const float* vbase = a.vc + (size_t)t0 * 512 + j * 256 + 4 * lane;
-    // 16 rows in flight per group; rows past cnt are clamped loads with p = 0 never added
-    for (int tg = 0; tg < cnt; tg += 16) {
-      float4 vv[16];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) vv[u] = *reinterpret_cast<const float4*>(vbase + (size_t)min(tg + u, cnt - 1) * 512);
+    for (int u = 0; u < kAttnSplit; ++u) {
+      if (u < cnt) {
+        const float v = (t0 + u == T) ? vT : vl[256 * u + t];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        if (tg + u < cnt) {   // position order (attention.hpp:80-86)
-          const float pv = pp[i][tg + u];
-          acc[0] = __builtin_fmaf(pv, vv[u].x, acc[0]);
-          acc[1] = __builtin_fmaf(pv, vv[u].y, acc[1]);
-          acc[2] = __builtin_fmaf(pv, vv[u].z, acc[2]);
-          acc[3] = __builtin_fmaf(pv, vv[u].w, acc[3]);
-        }
+        for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(pp[i][u], v, acc[i]);
       }
     }
-    stc4(a.pacc, ((4 * j + i) * a.nsplit_max + s) * 256 + 4 * lane, acc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) io.st1(a.pacc, a.part_st, ((4 * j + i) * a.nsplit_max + s) * 256 + t, acc[i]);
   }
   __syncthreads();
+  return true;
 }
 
 // Units u = blk, blk + nblk, ... of the 2 * ceil((T+1)/64) splits; T is the slot
 // of this token (past tokens = T).
-template <class Sync>
-__device__ __forceinline__ void attn_body(const AttnArgs& a, int T, int blk, int nblk, Sync& sync) {
+template <class IO>
+__device__ __forceinline__ bool attn_body(const AttnArgs& a, int T, int blk, int nblk, IO& io) {
   const bool ok = T >= 0 && T < a.max_ctx;
   const int units = ok ? 2 * ((T + 1 + kAttnSplit - 1) / kAttnSplit) : 0;
-  sync.arrive();
-  float kreg[4][16];
-  if (blk < units) attn_load_k(a, blk >> 1, blk & 1, T, kreg);
-  if (!sync.wait()) return;
+  io.arrive();
+  if (blk >= units) return true;
+  const int rrow = a.rope_row != nullptr ? ldc_i(a.rope_row) : T;
+  AttnPre pf;
+  attn_prefetch(a, blk >> 1, blk & 1, T, rrow, pf);
+  if (!io.wait()) return false;
   for (int u = blk; u < units; u += nblk) {
-    if (u != blk) attn_load_k(a, u >> 1, u & 1, T, kreg);
-    attn_unit(a, u >> 1, u & 1, T, kreg);
+    if (u != blk) attn_prefetch(a, u >> 1, u & 1, T, rrow, pf);
+    if (!attn_unit(a, u >> 1, u & 1, T, pf, io)) return false;
   }
+  return true;
 }
 
 // Merge the splits of head h in split order; output gate (attention.hpp:89-92).
-template <class Sync>
-__device__ __forceinline__ void combine_body(const AttnArgs& a, int T, int blk, Sync& sync) {
-  sync.arrive();
-  if (!sync.wait()) return;
+constexpr int kCombineChunk = 8;
+template <class IO>
+__device__ __forceinline__ bool combine_body(const AttnArgs& a, int T, int blk, IO& io) {
+  io.arrive();
+  if (!io.wait()) return false;
   const int h = blk, d = threadIdx.x;
-  if (h >= 8 || T < 0 || T >= a.max_ctx) return;
+  if (h >= 8 || T < 0 || T >= a.max_ctx) return true;
   const int Tn = T + 1;
   const int ns = (Tn + kAttnSplit - 1) / kAttnSplit;
-  const float* pm = a.pm + h * a.nsplit_max;
-  const float* pl = a.pl + h * a.nsplit_max;
+  const int base = h * a.nsplit_max;
   float M = -__builtin_inff();
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, ldcb(pm, s));
+  for (int s0 = 0; s0 < ns; s0 += kCombineChunk) {
+    int idx[kCombineChunk];
+    float m[kCombineChunk];
+#pragma unroll
+    for (int c = 0; c < kCombineChunk; ++c) idx[c] = base + min(s0 + c, ns - 1);
+    if (!io.template ldn<kCombineChunk>(a.pm, a.part_st, idx, m)) return false;
+#pragma unroll
+    for (int c = 0; c < kCombineChunk; ++c) M = fmaxf(M, m[c]);
+  }
   float L = 0.0f, ctx = 0.0f;
-  for (int s = 0; s < ns; ++s) {
-    const float e = dev_expf(ldcb(pm, s) - M);
-    L = L + ldcb(pl, s) * e;
-    ctx = ctx + ldcb(a.pacc, (h * a.nsplit_max + s) * 256 + d) * e;
+  for (int s0 = 0; s0 < ns; s0 += kCombineChunk) {
+    int idx[kCombineChunk], ia[kCombineChunk];
+    float m[kCombineChunk], l[kCombineChunk], pa[kCombineChunk];
+#pragma unroll
+    for (int c = 0; c < kCombineChunk; ++c) {
+      idx[c] = base + min(s0 + c, ns - 1);
+      ia[c] = idx[c] * 256 + d;
+    }
+    if (!io.template ldn<kCombineChunk>(a.pm, a.part_st, idx, m)) return false;
+    if (!io.template ldn<kCombineChunk>(a.pl, a.part_st, idx, l)) return false;
+    if (!io.template ldn<kCombineChunk>(a.pacc, a.part_st, ia, pa)) return false;
+#pragma unroll
+    for (int c = 0; c < kCombineChunk; ++c) {
+      if (s0 + c < ns) {
+        const float e = dev_expf(m[c] - M);
+        L = L + l[c] * e;
+        ctx = ctx + pa[c] * e;
+      }
+    }
   }
   const float invL = 1.0f / L;
-  const float gate = ldcb(a.qg, h * 512 + 256 + d);
-  stcb(a.og, h * 256 + d, (ctx * invL) * dev_sigmoid(gate));
+  float gate;
+  if (!io.ld1(a.qg, a.qkv_st, h * 512 + 256 + d, gate)) return false;
+  io.st1(a.og, a.og_st, h * 256 + d, (ctx * invL) * dev_sigmoid(gate));
+  return true;
 }
 
 }  // namespace qh
