@@ -86,23 +86,57 @@ __device__ __forceinline__ float dev_softplus(float x) {
   return x > 20.0f ? x : dev_log1pf(dev_expf(x));
 }
 
-// xor butterfly over groups of WIDTH lanes (offsets WIDTH/2 .. 1).
+// Lane l receives the value of lane l ^ OFF: quad permutations (DPP) for 1 and
+// 2, rotation of a 16-lane row by 8 (DPP row_ror) for 8, ds_swizzle's xor mode
+// (within 32 lanes) for 4 and 16, ds_bpermute only for 32.  Each is an exact
+// permutation, so a butterfly built from them is bit-identical to one built
+// from __shfl_xor.
+template <int OFF>
+__device__ __forceinline__ int xor_perm_i(int v) {
+  static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8 || OFF == 16 || OFF == 32, "xor offset");
+  if constexpr (OFF == 1) return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+  if constexpr (OFF == 2) return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+  if constexpr (OFF == 4) return __builtin_amdgcn_ds_swizzle(v, 0x101F);                     // and 0x1f, xor 4
+  if constexpr (OFF == 8) return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false);  // row_ror:8
+  if constexpr (OFF == 16) return __builtin_amdgcn_ds_swizzle(v, 0x401F);                    // and 0x1f, xor 16
+  if constexpr (OFF == 32) return __shfl_xor(v, 32, 64);
+  return v;
+}
+template <int OFF>
+__device__ __forceinline__ float xor_perm(float v) {
+  return __int_as_float(xor_perm_i<OFF>(__float_as_int(v)));
+}
+
+// xor butterfly over groups of WIDTH lanes (offsets WIDTH/2 .. 1); every lane
+// of a group ends with the same, fully determined value.
 template <int WIDTH>
 __device__ __forceinline__ float xor_sum(float v) {
-#pragma unroll
-  for (int off = WIDTH / 2; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
+  if constexpr (WIDTH >= 64) v = v + xor_perm<32>(v);
+  if constexpr (WIDTH >= 32) v = v + xor_perm<16>(v);
+  if constexpr (WIDTH >= 16) v = v + xor_perm<8>(v);
+  if constexpr (WIDTH >= 8) v = v + xor_perm<4>(v);
+  if constexpr (WIDTH >= 4) v = v + xor_perm<2>(v);
+  if constexpr (WIDTH >= 2) v = v + xor_perm<1>(v);
   return v;
 }
 template <int WIDTH>
 __device__ __forceinline__ int xor_sum_i(int v) {
-#pragma unroll
-  for (int off = WIDTH / 2; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
+  if constexpr (WIDTH >= 64) v = v + xor_perm_i<32>(v);
+  if constexpr (WIDTH >= 32) v = v + xor_perm_i<16>(v);
+  if constexpr (WIDTH >= 16) v = v + xor_perm_i<8>(v);
+  if constexpr (WIDTH >= 8) v = v + xor_perm_i<4>(v);
+  if constexpr (WIDTH >= 4) v = v + xor_perm_i<2>(v);
+  if constexpr (WIDTH >= 2) v = v + xor_perm_i<1>(v);
   return v;
 }
 template <int WIDTH>
 __device__ __forceinline__ float xor_max(float v) {
-#pragma unroll
-  for (int off = WIDTH / 2; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  if constexpr (WIDTH >= 64) v = fmaxf(v, xor_perm<32>(v));
+  if constexpr (WIDTH >= 32) v = fmaxf(v, xor_perm<16>(v));
+  if constexpr (WIDTH >= 16) v = fmaxf(v, xor_perm<8>(v));
+  if constexpr (WIDTH >= 8) v = fmaxf(v, xor_perm<4>(v));
+  if constexpr (WIDTH >= 4) v = fmaxf(v, xor_perm<2>(v));
+  if constexpr (WIDTH >= 2) v = fmaxf(v, xor_perm<1>(v));
   return v;
 }
 

@@ -41,9 +41,7 @@ struct qh_engine {
   float* o = nullptr;      // [2048]
   float* act = nullptr;    // [3584]
   float* og = nullptr;     // [2048]
-  float* qg = nullptr;     // [4096]
-  float* kraw = nullptr;   // [512]
-  float* vraw = nullptr;   // [512]
+  float* qkv = nullptr;    // [5120] q||gate | k | v
   float* pm = nullptr;
   float* pl = nullptr;
   float* pacc = nullptr;
@@ -124,6 +122,11 @@ struct Bufs {
     const size_t off = used;
     used += (n + 31) & ~(size_t)31;   // 256-byte aligned regions
     return arena != nullptr ? reinterpret_cast<float*>(arena + off) : nullptr;
+  }
+  // element n of a vector from take()
+  float* at(float* v, size_t n) const {
+    if (v == nullptr) return nullptr;
+    return tagged ? reinterpret_cast<float*>(reinterpret_cast<uint64_t*>(v) + n) : v + n;
   }
 };
 
@@ -238,21 +241,20 @@ void build_layers(const qh_engine* e, int l0, int l1, bool embed, Bufs& B, std::
       a.eps = kEps;
       a.done = done;
       a.nseg = 3;
-      a.seg[0] = mkseg(SEG_I8, E_STORE, kQProj, 0, B.take(kQProj, e->qg));
+      float* qkv = B.take(kQProj + 2 * kKVProj, e->qkv);   // q||gate | k | v
+      a.seg[0] = mkseg(SEG_I8, E_STORE, kQProj, 0, qkv);
       a.seg[0].w = i8p(e, l, R_QP);
       a.seg[0].sw = scp(e, l, R_QP);
-      a.seg[1] = mkseg(SEG_I8, E_STORE, kKVProj, a.seg[0].nbatch, B.take(kKVProj, e->kraw));
+      a.seg[1] = mkseg(SEG_I8, E_STORE, kKVProj, a.seg[0].nbatch, B.at(qkv, kQProj));
       a.seg[1].w = i8p(e, l, R_KP);
       a.seg[1].sw = scp(e, l, R_KP);
-      a.seg[2] = mkseg(SEG_I8, E_STORE, kKVProj, a.seg[1].batch0 + a.seg[1].nbatch, B.take(kKVProj, e->vraw));
+      a.seg[2] = mkseg(SEG_I8, E_STORE, kKVProj, a.seg[1].batch0 + a.seg[1].nbatch, B.at(qkv, kQProj + kKVProj));
       a.seg[2].w = i8p(e, l, R_VP);
       a.seg[2].sw = scp(e, l, R_VP);
       out.push_back(gemv_stage(ST_GEMV_NORM_1x8, a));
       const int sB = (int)out.size();
       AttnArgs at;
-      at.qg = a.seg[0].out;
-      at.kraw = a.seg[1].out;
-      at.vraw = a.seg[2].out;
+      at.qkv = qkv;
       at.qkv_st = sA;
       at.qn = f32p(e, l, R_QN);
       at.kn = f32p(e, l, R_KN);
@@ -549,7 +551,7 @@ void release(qh_engine* e) {
       for (auto& g : b)
         if (g) (void)hipGraphExecDestroy(g);
   void* bufs[] = {e->blob, e->rec, e->conv, e->kc, e->vc, e->h, e->convd, e->zb, e->gb, e->o, e->act,
-                  e->og, e->qg, e->kraw, e->vraw, e->pm, e->pl, e->pacc, e->rope, e->logits, e->part_val,
+                  e->og, e->qkv, e->pm, e->pl, e->pacc, e->rope, e->logits, e->part_val,
                   e->part_idx, e->ctl, e->prompt_dev, e->out_dev, e->prog[0], e->prog[1], e->arena,
                   e->abort_dev};
   for (void* p : bufs)
@@ -611,9 +613,7 @@ int create(const void* blob, size_t blob_len, const char* idx_text, int max_ctx,
   QH_C(dalloc(&e->o, kLH * kLV));
   QH_C(dalloc(&e->act, kInter));
   QH_C(dalloc(&e->og, kNH * kHD));
-  QH_C(dalloc(&e->qg, kQProj));
-  QH_C(dalloc(&e->kraw, kKVProj));
-  QH_C(dalloc(&e->vraw, kKVProj));
+  QH_C(dalloc(&e->qkv, kQProj + 2 * kKVProj));
   QH_C(dalloc(&e->pm, (size_t)8 * e->nsplit_max));
   QH_C(dalloc(&e->pl, (size_t)8 * e->nsplit_max));
   QH_C(dalloc(&e->pacc, (size_t)8 * e->nsplit_max * 256));

@@ -100,9 +100,7 @@ struct StepCtl {
 };
 
 struct AttnArgs {
-  const float* qg = nullptr;     // [4096] q || gate interleaved per head
-  const float* kraw = nullptr;   // [512]
-  const float* vraw = nullptr;   // [512]
+  const float* qkv = nullptr;    // [5120]: q || gate interleaved per head [4096], k [512], v [512]
   const float* qn = nullptr;     // q_norm [256]
   const float* kn = nullptr;     // k_norm [256]
   const float* rope = nullptr;   // [rows][64]: cos[32] then sin[32] per row
@@ -118,7 +116,7 @@ struct AttnArgs {
   float* og = nullptr;           // combine output [2048]
   float eps = 1e-6f;
   const int* done = nullptr;
-  int qkv_st = 0;                // producer of qg / kraw / vraw (tagged I/O)
+  int qkv_st = 0;                // producer of qkv (tagged I/O)
   int part_st = 0;               // attention stage: pm / pl / pacc
   int og_st = 0;                 // combine stage: og
 };

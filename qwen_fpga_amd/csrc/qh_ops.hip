@@ -158,11 +158,12 @@ int attention_layer(float* out, const float* x, const qh_tensor* q_w, const qh_t
   const int Tn = T + 1;
   const int ns = (Tn + kAttnSplit - 1) / kAttnSplit;
   Scratch sc(s);
-  QH_TRY(sc.alloc(rnd(4 * kQProj) + 2 * rnd(4 * kKVProj) + rnd(4 * 64) + rnd(8) + 2 * rnd(4 * 8 * (size_t)ns) +
+  QH_TRY(sc.alloc(rnd(4 * (kQProj + 2 * kKVProj)) + rnd(4 * 64) + rnd(8) + 2 * rnd(4 * 8 * (size_t)ns) +
                   rnd(4 * 8 * 256 * (size_t)ns) + rnd(4 * kNH * kHD)));
-  float* qg = sc.take<float>(kQProj);
-  float* kraw = sc.take<float>(kKVProj);
-  float* vraw = sc.take<float>(kKVProj);
+  float* qkv = sc.take<float>(kQProj + 2 * kKVProj);   // q||gate | k | v
+  float* qg = qkv;
+  float* kraw = qkv + kQProj;
+  float* vraw = qkv + kQProj + kKVProj;
   float* rope = sc.take<float>(64);
   int* ints = sc.take<int>(2);
   float* pm = sc.take<float>(8 * (size_t)ns);
@@ -184,9 +185,7 @@ int attention_layer(float* out, const float* x, const qh_tensor* q_w, const qh_t
   QH_HIP(launch_set_floats(rope, r, 64, s));
   QH_HIP(launch_set_ints(ints, T, 0, s));
   AttnArgs at;
-  at.qg = qg;
-  at.kraw = kraw;
-  at.vraw = vraw;
+  at.qkv = qkv;
   at.qn = q_norm;
   at.kn = k_norm;
   at.rope = rope;

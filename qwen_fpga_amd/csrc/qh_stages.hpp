@@ -28,6 +28,14 @@
 namespace qh {
 
 typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+
+template <int OFF, typename T>
+__device__ __forceinline__ T xperm(T v) {
+  if constexpr (sizeof(T) == 4 && __is_same(T, float))
+    return xor_perm<OFF>(v);
+  else
+    return xor_perm_i<OFF>(v);
+}
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
 
 // A value loaded before it is needed (epilogue residual): raw bits and tag.
@@ -91,6 +99,21 @@ struct PlainIO {
     stcb(reinterpret_cast<float*>(base), idx, __int_as_float(v));
   }
   __device__ __forceinline__ void st16(float* base, int, int idx, const float* v) { stc16(base, idx, v); }
+  // N 16-element chunks and one more element, all from one vector
+  template <int N>
+  __device__ __forceinline__ bool ld16v(const float* base, int st, const int (&idx)[N], float (&v)[N][16], int idx1,
+                                        float& v1) {
+    ld16<N>(base, st, idx, v);
+    v1 = ldcb(base, idx1);
+    return true;
+  }
+  // A vector the workgroup copied to LDS earlier in this stage program (none here).
+  __device__ __forceinline__ const float* cached(const float*, int) const { return nullptr; }
+  struct VecPoll {};
+  __device__ __forceinline__ void stage_issue(const float*, int, VecPoll&) {}
+  __device__ __forceinline__ bool stage_finish(const float* base, int st, int K, float* lds, VecPoll&) {
+    return stage_vec(base, st, K, lds);
+  }
   // The whole workgroup copies elements [0, K) (K a multiple of 4) into lds;
   // every thread must call it (it ends with a workgroup barrier).
   __device__ __forceinline__ bool stage_vec(const float* base, int, int K, float* lds) {
@@ -234,25 +257,84 @@ struct TagIO {
   __device__ __forceinline__ void st1i(int* base, int st, int idx, int v) {
     st1(reinterpret_cast<float*>(base), st, idx, __int_as_float(v));
   }
-  // The whole workgroup (kPersistThreads threads) copies elements [0, K) of a
-  // tagged vector into lds as fp32, K <= 4096 and even: every wave first polls
-  // 64 samples spread over the vector, then each thread loads its pairs (all
-  // loads in flight at once) until their tags match.  Ends with a barrier.
+  template <int N>
+  __device__ __forceinline__ bool ld16v(const float* base, int st, const int (&idx)[N], float (&v)[N][16], int idx1,
+                                        float& v1) {
+    const uint32_t tg = tag(st);
+    const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
+    unsigned polls = 0;
+    for (bool first = true;; first = false) {
+      if (!first && !sample(rs, idx1, tg, polls)) return false;
+      asm volatile("" ::: "memory");
+      u32x4 u[N][8];
+#pragma unroll
+      for (int j = 0; j < N; ++j)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) u[j][k] = __builtin_amdgcn_raw_buffer_load_b128(rs, (idx[j] + 2 * k) * 8, 0, kSc1);
+      const u32x2 u1 = __builtin_amdgcn_raw_buffer_load_b64(rs, idx1 * 8, 0, kSc1);
+      bool ok = u1[1] == tg;
+#pragma unroll
+      for (int j = 0; j < N; ++j)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) ok = ok & (u[j][k][1] == tg) & (u[j][k][3] == tg);
+      if (wave_all(ok)) {
+#pragma unroll
+        for (int j = 0; j < N; ++j)
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            v[j][2 * k] = __uint_as_float(u[j][k][0]);
+            v[j][2 * k + 1] = __uint_as_float(u[j][k][2]);
+          }
+        v1 = __uint_as_float(u1[0]);
+        return true;
+      }
+      if (!again(polls)) return false;
+    }
+  }
+  // The last vector this workgroup copied to LDS (stage_finish), if it is (base, st).
+  const float* last_base = nullptr;
+  int last_st = -1;
+  const float* last_lds = nullptr;
+  __device__ __forceinline__ const float* cached(const float* base, int st) const {
+    return (base == last_base && st == last_st) ? last_lds : nullptr;
+  }
+  // First poll of a workgroup copy, issued before the stage's weight loads so
+  // that its result does not queue behind them (loads return in order).
+  static constexpr int kL = 4096 / (2 * kPersistThreads);   // b128 loads per thread
+  struct VecPoll {
+    u32x4 u[kL];
+  };
+  __device__ __forceinline__ void stage_issue(const float* base, int K, VecPoll& vp) {
+    const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
+    const int t = threadIdx.x;
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < kL; ++i) {
+      const int p = min(2 * t + 2 * kPersistThreads * i, K - 2);
+      vp.u[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, p * 8, 0, kSc1);
+    }
+  }
   __device__ __forceinline__ bool stage_vec(const float* base, int st, int K, float* lds) {
-    constexpr int kL = 4096 / (2 * kPersistThreads);   // b128 loads per thread
+    VecPoll vp;
+    stage_issue(base, K, vp);
+    return stage_finish(base, st, K, lds, vp);
+  }
+  // The whole workgroup (kPersistThreads threads) copies elements [0, K) of a
+  // tagged vector into lds as fp32, K <= 4096 and even: each thread checks the
+  // tags of its pairs (first loads issued by stage_issue); after a miss every
+  // wave polls 64 samples spread over the vector before loading its pairs
+  // again.  Ends with a barrier.
+  __device__ __forceinline__ bool stage_finish(const float* base, int st, int K, float* lds, VecPoll& vp) {
     const uint32_t tg = tag(st);
     const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
     const int t = threadIdx.x, lane = t & 63;
     unsigned polls = 0;
     for (bool first = true;; first = false) {
-      if (!first && !sample(rs, (int)(((unsigned)(2 * lane + 1) * (unsigned)K) >> 7), tg, polls)) return false;
-      asm volatile("" ::: "memory");
-      u32x4 u[kL];
-#pragma unroll
-      for (int i = 0; i < kL; ++i) {
-        const int p = min(2 * t + 2 * kPersistThreads * i, K - 2);
-        u[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, p * 8, 0, kSc1);
+      if (!first) {
+        if (!sample(rs, (int)(((unsigned)(2 * lane + 1) * (unsigned)K) >> 7), tg, polls)) return false;
+        stage_issue(base, K, vp);
       }
+      const u32x4* u = vp.u;
       bool ok = true;
 #pragma unroll
       for (int i = 0; i < kL; ++i) ok = ok & (u[i][1] == tg) & (u[i][3] == tg);
@@ -267,6 +349,9 @@ struct TagIO {
       if (!again(polls)) return false;
     }
     __syncthreads();
+    last_base = base;
+    last_st = st;
+    last_lds = lds;
     return true;
   }
   __device__ __forceinline__ void st16(float* base, int st, int idx, const float* v) {
@@ -304,7 +389,7 @@ __device__ __forceinline__ T reduce8(T v[8], int lane) {
     for (int i = 0; i < 4; ++i) {
       const T send = up ? v[i] : v[i + 4];
       const T keep = up ? v[i + 4] : v[i];
-      v[i] = keep + __shfl_xor(send, 32, 64);
+      v[i] = keep + xperm<32>(send);
     }
   }
   {
@@ -313,19 +398,19 @@ __device__ __forceinline__ T reduce8(T v[8], int lane) {
     for (int i = 0; i < 2; ++i) {
       const T send = up ? v[i] : v[i + 2];
       const T keep = up ? v[i + 2] : v[i];
-      v[i] = keep + __shfl_xor(send, 16, 64);
+      v[i] = keep + xperm<16>(send);
     }
   }
   {
     const bool up = (lane & 8) != 0;
     const T send = up ? v[0] : v[1];
     const T keep = up ? v[1] : v[0];
-    v[0] = keep + __shfl_xor(send, 8, 64);
+    v[0] = keep + xperm<8>(send);
   }
   T r = v[0];
-  r = r + __shfl_xor(r, 4, 64);
-  r = r + __shfl_xor(r, 2, 64);
-  r = r + __shfl_xor(r, 1, 64);
+  r = r + xperm<4>(r);
+  r = r + xperm<2>(r);
+  r = r + xperm<1>(r);
   return r;
 }
 
@@ -337,20 +422,20 @@ __device__ __forceinline__ T reduce4(T v[4], int lane) {
     for (int i = 0; i < 2; ++i) {
       const T send = up ? v[i] : v[i + 2];
       const T keep = up ? v[i + 2] : v[i];
-      v[i] = keep + __shfl_xor(send, 32, 64);
+      v[i] = keep + xperm<32>(send);
     }
   }
   {
     const bool up = (lane & 16) != 0;
     const T send = up ? v[0] : v[1];
     const T keep = up ? v[1] : v[0];
-    v[0] = keep + __shfl_xor(send, 16, 64);
+    v[0] = keep + xperm<16>(send);
   }
   T r = v[0];
-  r = r + __shfl_xor(r, 8, 64);
-  r = r + __shfl_xor(r, 4, 64);
-  r = r + __shfl_xor(r, 2, 64);
-  r = r + __shfl_xor(r, 1, 64);
+  r = r + xperm<8>(r);
+  r = r + xperm<4>(r);
+  r = r + xperm<2>(r);
+  r = r + xperm<1>(r);
   return r;
 }
 
@@ -359,20 +444,24 @@ __device__ __forceinline__ T reduce2(T v[2], int lane) {
   const bool up = (lane & 32) != 0;
   const T send = up ? v[0] : v[1];
   const T keep = up ? v[1] : v[0];
-  T r = keep + __shfl_xor(send, 32, 64);
-  r = r + __shfl_xor(r, 16, 64);
-  r = r + __shfl_xor(r, 8, 64);
-  r = r + __shfl_xor(r, 4, 64);
-  r = r + __shfl_xor(r, 2, 64);
-  r = r + __shfl_xor(r, 1, 64);
+  T r = keep + xperm<32>(send);
+  r = r + xperm<16>(r);
+  r = r + xperm<8>(r);
+  r = r + xperm<4>(r);
+  r = r + xperm<2>(r);
+  r = r + xperm<1>(r);
   return r;
 }
 
 template <typename T>
 __device__ __forceinline__ T reduce1(T v[1], int) {
   T r = v[0];
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) r = r + __shfl_xor(r, off, 64);
+  r = r + xperm<32>(r);
+  r = r + xperm<16>(r);
+  r = r + xperm<8>(r);
+  r = r + xperm<4>(r);
+  r = r + xperm<2>(r);
+  r = r + xperm<1>(r);
   return r;
 }
 
@@ -467,7 +556,7 @@ __device__ __forceinline__ void gemv_epilogue(const Seg& g, int ost, int lane, i
   constexpr int LPR = 64 / R;   // lanes holding one row
   if constexpr (R >= 2) {
     if (g.epi == E_SWIGLU) {      // pair rows: even = gate i, odd = up i (mlp.hpp:17)
-      const float yo = __shfl_xor(y, LPR, 64);
+      const float yo = xperm<LPR>(y);
       if ((lane & (2 * LPR - 1)) == 0 && myrow < g.rows) io.st1(g.out, ost, myrow >> 1, dev_silu(y) * yo);
       return;
     }
@@ -551,7 +640,10 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
   io.arrive();
   io.mark(0);
   if (blk * nwv >= total) return true;   // no rows for this workgroup (workgroup-uniform)
-  // ---------------- 1. weights and epilogue inputs of the first batch in flight first
+  // ---------------- 1. the first poll of x, then weights and epilogue inputs of the first batch
+  const bool stage_x = PRO != P_LOADQ && !(PRO == P_NORM && a.emb != nullptr);
+  typename IO::VecPoll vx;
+  if (stage_x) io.stage_issue(a.x, K, vx);
   uint32_t w[NCH][R][4];
   EpiAux aux;
   int si = 0;
@@ -574,9 +666,9 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
   // the workgroup's copy of x (and z): every wave takes part, rows or not
   const float* xl = nullptr;
   const float* zl = nullptr;
-  if (PRO != P_LOADQ && !(PRO == P_NORM && a.emb != nullptr)) {
+  if (stage_x) {
     float* buf = io.slot();
-    if (!io.stage_vec(a.x, a.x_st, K, buf)) return false;
+    if (!io.stage_finish(a.x, a.x_st, K, buf, vx)) return false;
     xl = buf;
   }
   if constexpr (PRO == P_GATED) {
@@ -773,6 +865,8 @@ __device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, 
   int b = blk * nwv + wave;
   const int rl = (lane >> 3) & 7;
   io.arrive();
+  typename IO::VecPoll vh;
+  io.stage_issue(a.h, 1024, vh);
   uint32_t w0[8][4], w1[8][4];
   float sc0 = 0.0f, sc1 = 0.0f;
   if (b < total) head_load(a, b, lane, rl, w0, sc0);   // two batches in flight before the norm prologue
@@ -783,7 +877,7 @@ __device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, 
   if (!io.wait()) return false;
   {
     float* hl = io.slot();
-    if (!io.stage_vec(a.h, a.h_st, 1024, hl)) return false;
+    if (!io.stage_finish(a.h, a.h_st, 1024, hl, vh)) return false;
     load16f(hl + 16 * lane, xv);
   }
   io.mark(1);
@@ -874,6 +968,8 @@ __device__ __forceinline__ bool deltanet_gates(const DnArgs& a, int h, int tokv,
     const float es = a.emb_s[tok];
 #pragma unroll
     for (int e = 0; e < 16; ++e) xv[e] = i8_at(t4, e) * es;
+  } else if (const float* xl = io.cached(a.gx, a.gx_st)) {   // the in_proj stage's copy
+    load16f(xl + 16 * lane, xv);
   } else {
     int idx[1] = {16 * lane};
     float t1[1][16];
@@ -947,19 +1043,20 @@ __device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool va
     }
   }
   float vv;
-  if (!io.ld1(a.convd, a.convd_st, 4096 + h * 128 + v, vv)) return false;
-  if (wave < 2) {   // wave 0: q, wave 1: k; lanes 0..7 hold 16 elements each
-    const int src = (wave == 0 ? 0 : 2048) + h * 128;
+  float qk[16];   // wave 0: q, wave 1: k (waves 2, 3 read q too and drop it); lanes 0..7 hold 16 each
+  {
+    int idx[1] = {((wave & 1) ? 2048 : 0) + h * 128 + 16 * min(lane, 7)};
+    float t1[1][16];
+    if (!io.template ld16v<1>(a.convd, a.convd_st, idx, t1, 4096 + h * 128 + v, vv)) return false;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) qk[e] = t1[0][e];
+  }
+  if (wave < 2) {
     float x[16];
     float ss = 0.0f;
-    {   // every lane polls (lanes >= 8 re-read lane 7's chunk and drop it)
-      int idx[1] = {src + 16 * min(lane, 7)};
-      float t1[1][16];
-      if (!io.template ld16<1>(a.convd, a.convd_st, idx, t1)) return false;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) x[e] = lane < 8 ? t1[0][e] : 0.0f;
-      if (lane < 8) ss = dot16_f32(x, x, 0.0f);
-    }
+    for (int e = 0; e < 16; ++e) x[e] = lane < 8 ? qk[e] : 0.0f;
+    if (lane < 8) ss = dot16_f32(x, x, 0.0f);
     if (a.normalize) {
       ss = xor_sum<8>(ss);
       const float inv = 1.0f / sqrtf(ss + 1e-6f);   // deltanet.hpp:134
@@ -1056,11 +1153,15 @@ __device__ __forceinline__ bool deltanet_all(const DnArgs& a, int blk, int nblk,
 // (global_load_lds_dwordx4, no registers), row i of the split at vl + 256 i.
 struct AttnPre {
   float kreg[4][16];
-  float qn[16], kn[16], cs[16], sn[16];
 };
 __device__ __forceinline__ float* attn_vlds() {
   __shared__ float vl[kAttnSplit * 256];
   return vl;
+}
+// q_norm gain [256], k_norm gain [256], RoPE row [64] (cos[32], sin[32])
+__device__ __forceinline__ float* attn_clds() {
+  __shared__ float c[256 + 256 + 64];
+  return c;
 }
 __device__ __forceinline__ void attn_prefetch(const AttnArgs& a, int s, int j, int T, int rrow, AttnPre& pf) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -1081,14 +1182,15 @@ __device__ __forceinline__ void attn_prefetch(const AttnArgs& a, int s, int j, i
   for (int i = wave; i < nv; i += 4)
     __builtin_amdgcn_global_load_lds(static_cast<const void*>(a.vc + (size_t)(t0 + i) * 512 + j * 256 + 4 * lane),
                                      (__attribute__((address_space(3))) void*)(vl + 256 * i), 16, 0, kSc1);
-  load16f(a.qn + 16 * g16, pf.qn);
-  load16f(a.kn + 16 * g16, pf.kn);
-  // rope.hpp:30-41 touches dims 0..63: lane g16 < 4 uses cos/sin[(16 g16 + e) & 31]
-  const float* cs = a.rope + (size_t)rrow * 64 + 16 * (g16 & 1);
-  load16f(cs, pf.cs);
-  load16f(cs + 32, pf.sn);
+  float* c = attn_clds();   // constants straight to LDS as well
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  if (wave == 0) __builtin_amdgcn_global_load_lds(static_cast<const void*>(a.qn + 4 * lane), (lds_ptr)c, 16, 0, 0);
+  if (wave == 1) __builtin_amdgcn_global_load_lds(static_cast<const void*>(a.kn + 4 * lane), (lds_ptr)(c + 256), 16, 0, 0);
+  if (wave == 2)
+    __builtin_amdgcn_global_load_lds(static_cast<const void*>(a.rope + (size_t)rrow * 64 + lane), (lds_ptr)(c + 512), 4, 0, 0);
 }
 
+// nw16: this lane's 16 gains; cs16 / sn16: cos / sin[(16 g16 + e) & 31] (lanes g16 < 4 use them)
 __device__ __forceinline__ void qk_norm_rope(float* x, const float* nw16, float eps, int g16, const float* cs16,
                                              const float* sn16) {
   float ss = dot16_f32(x, x, 0.0f);
@@ -1099,7 +1201,7 @@ __device__ __forceinline__ void qk_norm_rope(float* x, const float* nw16, float 
   // rope.hpp:30-41 on dims 0..63 (lanes g16 = 0..3); partner dims +-32 live in lane g16 ^ 2
   float part[16];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) part[e] = __shfl_xor(x[e], 2, 64);
+  for (int e = 0; e < 16; ++e) part[e] = xor_perm<2>(x[e]);
   if (g16 < 4) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
@@ -1118,29 +1220,48 @@ __device__ __forceinline__ bool attn_unit(const AttnArgs& a, int s, int j, int T
   __shared__ float pp[4][64];
   const float* vl = attn_vlds();
   const int t0 = s * kAttnSplit;
+  // qkv = q||gate (4096, interleaved per head) | k (512) | v (512)
+  const bool owner = T / kAttnSplit == s;   // slot T lies in this split (attention.hpp:45-54)
   float q[4][16];
-  {
-    int idx[4];
+  float k[16];
+  float vT = 0.0f;
+  io.mark(0);
+  if (owner) {   // the four query heads, the new K row and V element in one poll
+    int idx[5];
 #pragma unroll
     for (int i = 0; i < 4; ++i) idx[i] = (4 * j + i) * 512 + 16 * g16;   // query half of head 4j+i (attention.hpp:40)
-    io.mark(0);
-    if (!io.template ld16<4>(a.qg, a.qkv_st, idx, q)) return false;
-    io.mark(1);
+    idx[4] = 4096 + j * 256 + 16 * g16;
+    float t5[5][16];
+    if (!io.template ld16v<5>(a.qkv, a.qkv_st, idx, t5, 4608 + j * 256 + t, vT)) return false;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qk_norm_rope(q[i], pf.qn, a.eps, g16, pf.cs, pf.sn);
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) q[i][e] = t5[i][e];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) k[e] = t5[4][e];
+  } else {
+    int idx[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) idx[i] = (4 * j + i) * 512 + 16 * g16;
+    if (!io.template ld16<4>(a.qkv, a.qkv_st, idx, q)) return false;
   }
-  float vT = 0.0f;
-  if (T / kAttnSplit == s) {   // slot T lies in this split (attention.hpp:45-54)
-    float k[16];
-    {
-      int idx[1] = {j * 256 + 16 * g16};
-      float t1[1][16];
-      if (!io.template ld16<1>(a.kraw, a.qkv_st, idx, t1)) return false;
+  io.mark(1);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // constants and V rows of this wave are in LDS
+  __syncthreads();
+  const float* cl = attn_clds();
+  {
+    float nw[16], cs[16], sn[16];
+    load16f(cl + 16 * g16, nw);
+    load16f(cl + 512 + 16 * (g16 & 1), cs);   // rope.hpp:30-41 uses cos/sin[(16 g16 + e) & 31]
+    load16f(cl + 544 + 16 * (g16 & 1), sn);
 #pragma unroll
-      for (int e = 0; e < 16; ++e) k[e] = t1[0][e];
-      qk_norm_rope(k, pf.kn, a.eps, g16, pf.cs, pf.sn);
+    for (int i = 0; i < 4; ++i) qk_norm_rope(q[i], nw, a.eps, g16, cs, sn);
+    if (owner) {
+      load16f(cl + 256 + 16 * g16, nw);
+      qk_norm_rope(k, nw, a.eps, g16, cs, sn);
     }
-    if (!io.ld1(a.vraw, a.qkv_st, j * 256 + t, vT)) return false;
+  }
+  if (owner) {
     if (wave == 0 && pg == 0) stc16(a.kc, T * 512 + j * 256 + 16 * g16, k);
     stcb(a.vc, T * 512 + j * 256 + t, vT);
 #pragma unroll
@@ -1176,7 +1297,6 @@ __device__ __forceinline__ bool attn_unit(const AttnArgs& a, int s, int j, int T
       io.st1(a.pl, a.part_st, (4 * j + i) * a.nsplit_max + s, l);
     }
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's V rows have reached LDS
   __syncthreads();
   {   // thread t = dimension; position order (attention.hpp:80-86)
     const int cnt = min(kAttnSplit, Tn - t0);
@@ -1259,7 +1379,7 @@ __device__ __forceinline__ bool combine_body(const AttnArgs& a, int T, int blk, 
   }
   const float invL = 1.0f / L;
   float gate;
-  if (!io.ld1(a.qg, a.qkv_st, h * 512 + 256 + d, gate)) return false;
+  if (!io.ld1(a.qkv, a.qkv_st, h * 512 + 256 + d, gate)) return false;
   io.st1(a.og, a.og_st, h * 256 + d, (ctx * invL) * dev_sigmoid(gate));
   return true;
 }
