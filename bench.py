@@ -28,6 +28,22 @@ FLOOR_BYTES = 758_248_704  # int8 payload + scales + fp32 tensors read per token
 HEAD_BYTES = 248320 * 1024 + 248320 * 4 + 2 * 4096   # int8 rows + scales + h + final-norm gain
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "head_kernel_decode_c5_pmc_traffic.md")
+
+
+def head_traffic():
+    """HBM bytes per head_kernel launch from the committed rocprofv3 counter
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by a copy of known size); the
+    counters cannot be read from inside this process."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def full_bytes(T: int) -> int:
     """Algorithmic bytes of one token with T cached positions: weights + DeltaNet
     state r/w + conv history r/w + KV read (T+1 rows) and write."""
@@ -130,7 +146,7 @@ def main() -> int:
             "peak": PEAK_GBS,
             "unit": "GB/s",
             "frac": round(head_gbs / PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": head_traffic(),
             "duration_us": round(head_ms * 1e3, 2),
             "bytes_per_launch": HEAD_BYTES,
             "stream_step_ms": round(step_ms, 4),
