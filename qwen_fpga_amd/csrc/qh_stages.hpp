@@ -45,6 +45,12 @@ struct Raw {
 
 __device__ __forceinline__ bool wave_all(bool ok) { return __builtin_amdgcn_ballot_w64(!ok) == 0; }
 
+// Buffer descriptor over n bytes at base; n = 0 makes every access a no-op
+// that reads 0, so optional loads can be issued without a branch.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_n(const void* base, int n) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+
 // Workgroup copies of handed-over vectors (GEMV inputs, the LM head's h): a
 // ring of four 4096-float slots.  A workgroup takes the slots in order, one or
 // two per stage, and each copy ends with a workgroup barrier, so a slot is
@@ -85,9 +91,9 @@ struct PlainIO {
     v = __float_as_int(ldcb(reinterpret_cast<const float*>(base), idx));
     return true;
   }
-  __device__ __forceinline__ Raw issue1(const float* base, int idx) {
+  __device__ __forceinline__ Raw issue1(const float* base, int idx, bool valid = true) {
     Raw r;
-    r.v = __float_as_uint(ldcb(base, idx));
+    r.v = __builtin_amdgcn_raw_buffer_load_b32(rsrc_n(base, valid ? 0x7ffffff0 : 0), idx * 4, 0, kSc1);
     return r;
   }
   __device__ __forceinline__ bool resolve1(const Raw& r, const float*, int, int, float& v) {
@@ -167,59 +173,75 @@ struct TagIO {
       if (!again(polls)) return false;
     }
   }
+  // The first load of every wait is checked outside the retry loop, so the
+  // compiler can wait for exactly that load (and not for loads issued after it).
+  template <int N>
+  __device__ __forceinline__ static void issue16(const __amdgpu_buffer_rsrc_t& rs, const int (&idx)[N], u32x4 (&u)[N][8]) {
+    asm volatile("" ::: "memory");   // re-issue the loads on every poll
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) u[j][k] = __builtin_amdgcn_raw_buffer_load_b128(rs, (idx[j] + 2 * k) * 8, 0, kSc1);
+  }
+  template <int N>
+  __device__ __forceinline__ static bool tags16(const u32x4 (&u)[N][8], uint32_t tg) {
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) ok = ok & (u[j][k][1] == tg) & (u[j][k][3] == tg);
+    return wave_all(ok);
+  }
   template <int N>
   __device__ __forceinline__ bool ld16(const float* base, int st, const int (&idx)[N], float (&v)[N][16]) {
     const uint32_t tg = tag(st);
     const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
-    unsigned polls = 0;
-    for (bool first = true;; first = false) {
-      // after a miss, wait on one pair per lane before loading everything again
-      if (!first && !sample(rs, idx[N - 1] + 15, tg, polls)) return false;
-      asm volatile("" ::: "memory");   // re-issue the loads on every poll
-      u32x4 u[N][8];
-#pragma unroll
-      for (int j = 0; j < N; ++j)
-#pragma unroll
-        for (int k = 0; k < 8; ++k) u[j][k] = __builtin_amdgcn_raw_buffer_load_b128(rs, (idx[j] + 2 * k) * 8, 0, kSc1);
-      bool ok = true;
-#pragma unroll
-      for (int j = 0; j < N; ++j)
-#pragma unroll
-        for (int k = 0; k < 8; ++k) ok = ok & (u[j][k][1] == tg) & (u[j][k][3] == tg);
-      if (wave_all(ok)) {
-#pragma unroll
-        for (int j = 0; j < N; ++j)
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            v[j][2 * k] = __uint_as_float(u[j][k][0]);
-            v[j][2 * k + 1] = __uint_as_float(u[j][k][2]);
-          }
-        return true;
-      }
-      if (!again(polls)) return false;
+    u32x4 u[N][8];
+    issue16<N>(rs, idx, u);
+    if (!tags16<N>(u, tg)) {
+      unsigned polls = 0;
+      do {   // after a miss, wait on one pair per lane before loading everything again
+        if (!again(polls) || !sample(rs, idx[N - 1] + 15, tg, polls)) return false;
+        issue16<N>(rs, idx, u);
+      } while (!tags16<N>(u, tg));
     }
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        v[j][2 * k] = __uint_as_float(u[j][k][0]);
+        v[j][2 * k + 1] = __uint_as_float(u[j][k][2]);
+      }
+    return true;
   }
   template <int N>
   __device__ __forceinline__ bool ldn(const float* base, int st, const int (&idx)[N], float (&v)[N]) {
     const uint32_t tg = tag(st);
     const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
-    unsigned polls = 0;
-    for (bool first = true;; first = false) {
-      if (N > 1 && !first && !sample(rs, idx[N - 1], tg, polls)) return false;
+    u32x2 u[N];
+    auto issue = [&]() {
       asm volatile("" ::: "memory");
-      u32x2 u[N];
 #pragma unroll
       for (int j = 0; j < N; ++j) u[j] = __builtin_amdgcn_raw_buffer_load_b64(rs, idx[j] * 8, 0, kSc1);
+    };
+    auto tags = [&]() {
       bool ok = true;
 #pragma unroll
       for (int j = 0; j < N; ++j) ok = ok & (u[j][1] == tg);
-      if (wave_all(ok)) {
-#pragma unroll
-        for (int j = 0; j < N; ++j) v[j] = __uint_as_float(u[j][0]);
-        return true;
-      }
-      if (!again(polls)) return false;
+      return wave_all(ok);
+    };
+    issue();
+    if (!tags()) {
+      unsigned polls = 0;
+      do {
+        if (!again(polls)) return false;
+        if (N > 1 && !sample(rs, idx[N - 1], tg, polls)) return false;
+        issue();
+      } while (!tags());
     }
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] = __uint_as_float(u[j][0]);
+    return true;
   }
   __device__ __forceinline__ bool ld1(const float* base, int st, int idx, float& v) {
     int i1[1] = {idx};
@@ -234,8 +256,8 @@ struct TagIO {
     v = __float_as_int(f);
     return ok;
   }
-  __device__ __forceinline__ Raw issue1(const float* base, int idx) {
-    const u32x2 u = __builtin_amdgcn_raw_buffer_load_b64(coh_rsrc(base), idx * 8, 0, kSc1);
+  __device__ __forceinline__ Raw issue1(const float* base, int idx, bool valid = true) {
+    const u32x2 u = __builtin_amdgcn_raw_buffer_load_b64(rsrc_n(base, valid ? 0x7ffffff0 : 0), idx * 8, 0, kSc1);
     Raw r;
     r.v = u[0];
     r.t = u[1];
@@ -262,34 +284,30 @@ struct TagIO {
                                         float& v1) {
     const uint32_t tg = tag(st);
     const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
-    unsigned polls = 0;
-    for (bool first = true;; first = false) {
-      if (!first && !sample(rs, idx1, tg, polls)) return false;
-      asm volatile("" ::: "memory");
-      u32x4 u[N][8];
-#pragma unroll
-      for (int j = 0; j < N; ++j)
-#pragma unroll
-        for (int k = 0; k < 8; ++k) u[j][k] = __builtin_amdgcn_raw_buffer_load_b128(rs, (idx[j] + 2 * k) * 8, 0, kSc1);
-      const u32x2 u1 = __builtin_amdgcn_raw_buffer_load_b64(rs, idx1 * 8, 0, kSc1);
-      bool ok = u1[1] == tg;
-#pragma unroll
-      for (int j = 0; j < N; ++j)
-#pragma unroll
-        for (int k = 0; k < 8; ++k) ok = ok & (u[j][k][1] == tg) & (u[j][k][3] == tg);
-      if (wave_all(ok)) {
-#pragma unroll
-        for (int j = 0; j < N; ++j)
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            v[j][2 * k] = __uint_as_float(u[j][k][0]);
-            v[j][2 * k + 1] = __uint_as_float(u[j][k][2]);
-          }
-        v1 = __uint_as_float(u1[0]);
-        return true;
-      }
-      if (!again(polls)) return false;
+    u32x4 u[N][8];
+    u32x2 u1;
+    auto issue = [&]() {
+      issue16<N>(rs, idx, u);
+      u1 = __builtin_amdgcn_raw_buffer_load_b64(rs, idx1 * 8, 0, kSc1);
+    };
+    auto tags = [&]() { return tags16<N>(u, tg) & wave_all(u1[1] == tg); };
+    issue();
+    if (!tags()) {
+      unsigned polls = 0;
+      do {
+        if (!again(polls) || !sample(rs, idx1, tg, polls)) return false;
+        issue();
+      } while (!tags());
     }
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        v[j][2 * k] = __uint_as_float(u[j][k][0]);
+        v[j][2 * k + 1] = __uint_as_float(u[j][k][2]);
+      }
+    v1 = __uint_as_float(u1[0]);
+    return true;
   }
   // The last vector this workgroup copied to LDS (stage_finish), if it is (base, st).
   const float* last_base = nullptr;
@@ -304,15 +322,17 @@ struct TagIO {
   struct VecPoll {
     u32x4 u[kL];
   };
+  // K = 0 issues no memory access (empty descriptor).
   __device__ __forceinline__ void stage_issue(const float* base, int K, VecPoll& vp) {
-    const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
+    const __amdgpu_buffer_rsrc_t rs = rsrc_n(base, 8 * K);
     const int t = threadIdx.x;
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int i = 0; i < kL; ++i) {
-      const int p = min(2 * t + 2 * kPersistThreads * i, K - 2);
+      const int p = min(2 * t + 2 * kPersistThreads * i, max(K - 2, 0));
       vp.u[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, p * 8, 0, kSc1);
     }
+    asm volatile("" ::: "memory");   // nothing issued later may move ahead of these loads
   }
   __device__ __forceinline__ bool stage_vec(const float* base, int st, int K, float* lds) {
     VecPoll vp;
@@ -324,29 +344,36 @@ struct TagIO {
   // tags of its pairs (first loads issued by stage_issue); after a miss every
   // wave polls 64 samples spread over the vector before loading its pairs
   // again.  Ends with a barrier.
+  __device__ __forceinline__ static bool vec_tags(const VecPoll& vp, int K, uint32_t tg) {
+    const int t = threadIdx.x;
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < kL; ++i) {
+      const bool in = 2 * t + 2 * kPersistThreads * i < K;   // clamped duplicates are checked too: harmless
+      ok = ok & (!in | ((vp.u[i][1] == tg) & (vp.u[i][3] == tg)));
+    }
+    return wave_all(ok);
+  }
   __device__ __forceinline__ bool stage_finish(const float* base, int st, int K, float* lds, VecPoll& vp) {
     const uint32_t tg = tag(st);
-    const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
     const int t = threadIdx.x, lane = t & 63;
-    unsigned polls = 0;
-    for (bool first = true;; first = false) {
-      if (!first) {
-        if (!sample(rs, (int)(((unsigned)(2 * lane + 1) * (unsigned)K) >> 7), tg, polls)) return false;
+    if (!vec_tags(vp, K, tg)) {
+      const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
+      // 16 sampled lines per wave (lanes in groups of 4 share one), rotated per
+      // workgroup so that the waiting workgroups spread their polls over the
+      // whole vector instead of hammering the same few lines.
+      const unsigned k2 = (unsigned)K >> 1;   // 16-byte units
+      const unsigned sidx = (((unsigned)(lane >> 2) * k2) / 16u + 7u * (unsigned)blockIdx.x) % k2;
+      unsigned polls = 0;
+      do {
+        if (!again(polls) || !sample(rs, (int)(2 * sidx + 1), tg, polls)) return false;
         stage_issue(base, K, vp);
-      }
-      const u32x4* u = vp.u;
-      bool ok = true;
+      } while (!vec_tags(vp, K, tg));
+    }
 #pragma unroll
-      for (int i = 0; i < kL; ++i) ok = ok & (u[i][1] == tg) & (u[i][3] == tg);
-      if (wave_all(ok)) {
-#pragma unroll
-        for (int i = 0; i < kL; ++i) {
-          const int p = 2 * t + 2 * kPersistThreads * i;
-          if (p < K) *reinterpret_cast<float2*>(lds + p) = make_float2(__uint_as_float(u[i][0]), __uint_as_float(u[i][2]));
-        }
-        break;
-      }
-      if (!again(polls)) return false;
+    for (int i = 0; i < kL; ++i) {
+      const int p = 2 * t + 2 * kPersistThreads * i;
+      if (p < K) *reinterpret_cast<float2*>(lds + p) = make_float2(__uint_as_float(vp.u[i][0]), __uint_as_float(vp.u[i][2]));
     }
     __syncthreads();
     last_base = base;
@@ -520,33 +547,33 @@ struct EpiAux {
   float sc = 1.0f;                                     // the row's weight scale (int8 segments)
   Raw res;                                             // E_RESID: residual, resolved before use
 };
+// Every input an epilogue may need, loaded without a branch: inputs the
+// segment's epilogue does not use come from zero-size descriptors (no memory
+// access), so the load block stays straight-line and the compiler can count
+// outstanding loads exactly.
 template <class IO>
 __device__ __forceinline__ void epi_prefetch(const Seg& g, int myrow, EpiAux& x, IO& io) {
+  constexpr int kBig = 0x7ffffff0;
   const int r = min(myrow, g.rows - 1);   // always a valid address; unused rows are never stored
-  if (g.kind != SEG_F32) x.sc = seg_scale(g, r);
-  switch (g.epi) {
-    case E_RESID:
-      x.res = io.issue1(g.res, r);   // residual: written by another workgroup
-      break;
-    case E_GATE_A:
-      x.a0 = g.c0[r];
-      x.w0 = g.c1[r];
-      break;
-    case E_CONV: {
-      const float4 st = *reinterpret_cast<const float4*>(g.c2 + (size_t)r * 4);
-      const float4 w = *reinterpret_cast<const float4*>(g.c0 + (size_t)r * 4);
-      x.a1 = st.y;
-      x.a2 = st.z;
-      x.a3 = st.w;
-      x.w0 = w.x;
-      x.w1 = w.y;
-      x.w2 = w.z;
-      x.w3 = w.w;
-      break;
-    }
-    default:
-      break;
-  }
+  const bool pair = g.kind == SEG_PAIR;
+  const float* swp = (pair && (r & 1)) ? g.sw2 : g.sw;
+  const float sc = __uint_as_float(
+      __builtin_amdgcn_raw_buffer_load_b32(rsrc_n(swp, g.kind == SEG_F32 ? 0 : kBig), (pair ? (r >> 1) : r) * 4, 0, 0));
+  x.sc = g.kind == SEG_F32 ? 1.0f : sc;
+  x.res = io.issue1(g.res, r, g.epi == E_RESID);   // residual: written by another workgroup
+  const bool ga = g.epi == E_GATE_A, cv = g.epi == E_CONV;
+  const float a_log = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_n(g.c0, ga ? kBig : 0), r * 4, 0, 0));
+  const float dtb = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_n(g.c1, ga ? kBig : 0), r * 4, 0, 0));
+  const u32x4 st = __builtin_amdgcn_raw_buffer_load_b128(rsrc_n(g.c2, cv ? kBig : 0), r * 16, 0, 0);
+  const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rsrc_n(g.c0, cv ? kBig : 0), r * 16, 0, 0);
+  x.a0 = a_log;   // E_GATE_A: A_log (E_RESID overwrites a0 once the residual resolves)
+  x.w0 = ga ? dtb : __uint_as_float(w[0]);
+  x.a1 = __uint_as_float(st[1]);
+  x.a2 = __uint_as_float(st[2]);
+  x.a3 = __uint_as_float(st[3]);
+  x.w1 = __uint_as_float(w[1]);
+  x.w2 = __uint_as_float(w[2]);
+  x.w3 = __uint_as_float(w[3]);
 }
 
 // Row-batch epilogue: the writer lane of each row stores its result y.
@@ -600,22 +627,29 @@ __device__ __forceinline__ void gemv_epilogue(const Seg& g, int ost, int lane, i
 // Loads of one batch: every address is clamped into the segment (rows) and the
 // vector (chunks), so the loads are unconditional and issue back to back.  A
 // clamped chunk meets x = 0 (the prologue zeroes chunks beyond K) and a clamped
-// row is never stored, so neither changes a result.
+// row is never stored, so neither changes a result.  An fp32 segment has no
+// int8 rows: its descriptors are empty and the loads read nothing.
 template <int NCH, int R>
 __device__ __forceinline__ void load_batch(const Seg& g, int row0, int K, int nchunk, int lane,
                                            uint32_t (&w)[NCH][R][4]) {
   const bool pair = g.kind == SEG_PAIR;
-  const int8_t* w0 = g.w;
-  const int8_t* w1 = pair ? g.w2 : g.w;
+  const int n = g.kind == SEG_F32 ? 0 : 0x7ffffff0;
+  const __amdgpu_buffer_rsrc_t ra = rsrc_n(g.w, n);
+  const __amdgpu_buffer_rsrc_t rb = rsrc_n(pair ? g.w2 : g.w, n);
   const int last = g.rows - 1;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int row = min(row0 + r, last);
-    const int8_t* base = pair ? (((row & 1) ? w1 : w0) + (size_t)(row >> 1) * K) : (w0 + (size_t)row * K);
+    const int row = min(row0 + r, last);   // wave-uniform
+    const bool second = pair && (row & 1);
+    const int roff = (pair ? (row >> 1) : row) * K;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int c = min(lane + 64 * j, nchunk - 1);
-      load16b(base + 16 * c, w[j][r]);
+      const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(second ? rb : ra, roff + 16 * c, 0, 0);
+      w[j][r][0] = t[0];
+      w[j][r][1] = t[1];
+      w[j][r][2] = t[2];
+      w[j][r][3] = t[3];
     }
   }
 }
@@ -638,20 +672,22 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
   int b = blk * nwv + wave;
 
   io.arrive();
-  io.mark(0);
   if (blk * nwv >= total) return true;   // no rows for this workgroup (workgroup-uniform)
   // ---------------- 1. the first poll of x, then weights and epilogue inputs of the first batch
+  // One straight-line block issues every load of the first batch: the first
+  // poll of x, the weights, the epilogue inputs and the norm gains.  Waves
+  // without rows load the workgroup's last batch and drop it.
   const bool stage_x = PRO != P_LOADQ && !(PRO == P_NORM && a.emb != nullptr);
+  const int bq = min(b, total - 1);
+  int si = seg_of(a, bq);
   typename IO::VecPoll vx;
-  if (stage_x) io.stage_issue(a.x, K, vx);
+  if constexpr (PRO != P_LOADQ) io.stage_issue(a.x, stage_x ? K : 0, vx);
   uint32_t w[NCH][R][4];
   EpiAux aux;
-  int si = 0;
-  if (b < total) {
-    si = seg_of(a, b);
+  {
     const Seg& g = a.seg[si];
-    const int row0 = (b - g.batch0) * R;
-    if (g.kind != SEG_F32) load_batch<NCH, R>(g, row0, K, nchunk, lane, w);
+    const int row0 = (bq - g.batch0) * R;
+    load_batch<NCH, R>(g, row0, K, nchunk, lane, w);   // SEG_F32: never read
     epi_prefetch(g, row0 + row_of_lane<R>(lane), aux, io);
   }
   float nwv16[NCH][16];   // norm gains: constants, loaded before the hand-over wait
@@ -676,7 +712,6 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
     if (!io.stage_vec(a.z, a.z_st, K, buf)) return false;
     zl = buf;
   }
-  io.mark(1);
   if (b >= total) return true;   // no rows for this wave (block 0 / wave 0 always has some)
 
   // ---------------- 2. prologue: this lane's chunks c = lane + 64 j of x
@@ -834,7 +869,6 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
     si = sin;
     aux = auxn;
   }
-  io.mark(2);
   return true;
 }
 
@@ -873,14 +907,12 @@ __device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, 
   if (b + stride < total) head_load(a, b + stride, lane, rl, w1, sc1);
   float xv[16], nw[16];
   load16f(a.nw + 16 * lane, nw);
-  io.mark(0);
   if (!io.wait()) return false;
   {
     float* hl = io.slot();
     if (!io.stage_finish(a.h, a.h_st, 1024, hl, vh)) return false;
     load16f(hl + 16 * lane, xv);
   }
-  io.mark(1);
   float ss = dot16_f32(xv, xv, 0.0f);
   ss = xor_sum<64>(ss);
   const float inv = 1.0f / sqrtf(ss / 1024.0f + a.eps);
@@ -918,7 +950,6 @@ __device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, 
       }
     }
   }
-  io.mark(2);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     const float ov = __shfl_xor(bv, off, 64);
@@ -1028,7 +1059,6 @@ __device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool va
       }
     }
   }
-  io.mark(0);
   if (!ok) return false;
   if (!io.wait()) return false;
   if (!valid) return true;
@@ -1071,7 +1101,6 @@ __device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool va
     if (lane < 8) store16f((wave == 0 ? qs : ks) + 16 * lane, x);
   }
   __syncthreads();
-  io.mark(1);
   if (a.wa != nullptr) {
     g = gbs[0];
     beta = gbs[1];
@@ -1118,7 +1147,6 @@ __device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool va
       for (int gi = 0; gi < off; ++gi) pp[gi] = pp[gi] + pp[gi + off];
     io.st1(a.o, a.o_st, h * 128 + v, pp[0]);
   }
-  io.mark(2);
   __syncthreads();
   return true;
 }
@@ -1225,7 +1253,6 @@ __device__ __forceinline__ bool attn_unit(const AttnArgs& a, int s, int j, int T
   float q[4][16];
   float k[16];
   float vT = 0.0f;
-  io.mark(0);
   if (owner) {   // the four query heads, the new K row and V element in one poll
     int idx[5];
 #pragma unroll
@@ -1245,7 +1272,6 @@ __device__ __forceinline__ bool attn_unit(const AttnArgs& a, int s, int j, int T
     for (int i = 0; i < 4; ++i) idx[i] = (4 * j + i) * 512 + 16 * g16;
     if (!io.template ld16<4>(a.qkv, a.qkv_st, idx, q)) return false;
   }
-  io.mark(1);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // constants and V rows of this wave are in LDS
   __syncthreads();
   const float* cl = attn_clds();
@@ -1282,7 +1308,6 @@ __device__ __forceinline__ bool attn_unit(const AttnArgs& a, int s, int j, int T
       if (g16 == 0) sc[i][tl] = valid ? d * 0.0625f : -__builtin_inff();
     }
   }
-  io.mark(2);
   __syncthreads();
   {
     const int i = wave;
