@@ -10,8 +10,9 @@ with seeded synthetic int8 weights in the packed pack_weights.py layout; a
 the token fed back on the device.
 
 Prints one JSON line with tok/s, the achieved HBM bandwidth per token against
-the 8 TB/s MI355X peak, the roofline of the dominant kernel (the LM head, timed
-with HIP events on the engine stream), and the reference CPU path (the
+the 8 TB/s MI355X peak, the roofline of the dominant kernel (the LM head in
+its decode-step context, timed with HIP events on the engine stream that are
+stamped at the kernel's own start and end), and the reference CPU path (the
 reference's hls/src decode top compiled natively, one core) on a bounded sample.
 """
 import argparse
@@ -108,7 +109,8 @@ def main() -> int:
     mean_full = sum(full_bytes(T0 + i) for i in range(args.steps)) / args.steps
     achieved_gbs = FLOOR_BYTES * tok_s / 1e9
 
-    # dominant kernel: the LM head, HIP events on the engine stream, in-step context
+    # dominant kernel: the LM head inside each profiled step (after the 24 layers,
+    # so its weights are not cache-resident), HIP events stamped at kernel start / end
     step_ms, head_ms = eng.profile(args.profile_steps)
     head_gbs = HEAD_BYTES / (head_ms * 1e-3) / 1e9
 

@@ -225,7 +225,9 @@ int qh_engine_forward_layers(qh_engine* e, int l0, int l1, float* h);
 /* Measurement hook: runs n_steps decode steps as plain stream launches (the
  * kernels of the step graph, each fed the current token) and returns the mean
  * step time and the mean duration of the LM-head kernel, both from HIP events
- * on the engine stream.  Advances pos like n_steps decode_token calls. */
+ * on the engine stream; the head's events are stamped at the kernel's own start
+ * and end (hipExtLaunchKernel), so its duration excludes the dispatch gap.
+ * Advances pos like n_steps decode_token calls. */
 int qh_engine_profile(qh_engine* e, int n_steps, float* step_ms, float* head_ms);
 /* The engine's HIP stream (a hipStream_t). */
 void* qh_engine_stream(qh_engine* e);

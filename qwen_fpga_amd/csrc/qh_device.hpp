@@ -86,9 +86,26 @@ __device__ __forceinline__ float dev_softplus(float x) {
   return x > 20.0f ? x : dev_log1pf(dev_expf(x));
 }
 
-// Lane l receives the value of lane l ^ OFF: quad permutations (DPP) for 1 and
-// 2, rotation of a 16-lane row by 8 (DPP row_ror) for 8, ds_swizzle's xor mode
-// (within 32 lanes) for 4 and 16, ds_bpermute only for 32.  Each is an exact
+// gfx950's permlane swaps, written as inline assembly with both registers as
+// in/out operands: v_permlane32_swap a, b exchanges the upper 32 lanes of a with
+// the lower 32 lanes of b (afterwards a = [a.lo, b.lo], b = [a.hi, b.hi]);
+// v_permlane16_swap does the same for the odd 16-lane rows of a and the even
+// rows of b (a = [a.r0, b.r0, a.r2, b.r2], b = [a.r1, b.r1, a.r3, b.r3]).  The
+// s_nop pairs cover the VALU-write / permlane-read wait states, which the
+// compiler does not insert around inline assembly.  (The two-result builtin
+// is not used: this compiler folds its second result into the first when both
+// feed arithmetic.)
+__device__ __forceinline__ void permlane32_swap(unsigned& a, unsigned& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void permlane16_swap(unsigned& a, unsigned& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+
+// Lane l receives the value of lane l ^ OFF, with VALU instructions only (no
+// LDS round trip): quad permutations (DPP) for 1 and 2; row_half_mirror
+// (l ^ 7) then quad_perm [3,2,1,0] (l ^ 3) for 4; rotation of a 16-lane row by
+// 8 (DPP row_ror) for 8; a permlane swap for 16 and 32.  Each is an exact
 // permutation, so a butterfly built from them is bit-identical to one built
 // from __shfl_xor.
 template <int OFF>
@@ -96,23 +113,47 @@ __device__ __forceinline__ int xor_perm_i(int v) {
   static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8 || OFF == 16 || OFF == 32, "xor offset");
   if constexpr (OFF == 1) return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
   if constexpr (OFF == 2) return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
-  if constexpr (OFF == 4) return __builtin_amdgcn_ds_swizzle(v, 0x101F);                     // and 0x1f, xor 4
+  if constexpr (OFF == 4) {
+    const int t = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);                 // row_half_mirror
+    return __builtin_amdgcn_update_dpp(0, t, 0x1B, 0xF, 0xF, false);                         // quad_perm [3,2,1,0]
+  }
   if constexpr (OFF == 8) return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false);  // row_ror:8
-  if constexpr (OFF == 16) return __builtin_amdgcn_ds_swizzle(v, 0x401F);                    // and 0x1f, xor 16
-  if constexpr (OFF == 32) return __shfl_xor(v, 32, 64);
-  return v;
+  unsigned a = (unsigned)v, b = (unsigned)v;
+  if constexpr (OFF == 16) {
+    permlane16_swap(a, b);   // a = v of the even row of each pair, b = v of the odd row
+    return (int)((threadIdx.x & 16) ? a : b);
+  }
+  permlane32_swap(a, b);     // a = lower half of v (both halves), b = upper half
+  return (int)((threadIdx.x & 32) ? a : b);
 }
 template <int OFF>
 __device__ __forceinline__ float xor_perm(float v) {
   return __int_as_float(xor_perm_i<OFF>(__float_as_int(v)));
 }
 
+// One level of a transposed butterfly at offset 16 or 32: every lane keeps
+// `lo` if its bit OFF is clear and `hi` if it is set, and adds the value its
+// partner (lane ^ OFF) does not keep.  One permlane swap of (lo, hi) places
+// both addends of every lane in its two registers, so the level costs one
+// swap and one add; the sum equals keep + partner's send (commuted on the
+// upper lanes, which IEEE addition does not notice).
+template <int OFF, typename T>
+__device__ __forceinline__ T swap_add(T lo, T hi) {
+  static_assert(OFF == 16 || OFF == 32, "swap level");
+  unsigned a = __builtin_bit_cast(unsigned, lo), b = __builtin_bit_cast(unsigned, hi);
+  if constexpr (OFF == 16)
+    permlane16_swap(a, b);
+  else
+    permlane32_swap(a, b);
+  return __builtin_bit_cast(T, a) + __builtin_bit_cast(T, b);
+}
+
 // xor butterfly over groups of WIDTH lanes (offsets WIDTH/2 .. 1); every lane
 // of a group ends with the same, fully determined value.
 template <int WIDTH>
 __device__ __forceinline__ float xor_sum(float v) {
-  if constexpr (WIDTH >= 64) v = v + xor_perm<32>(v);
-  if constexpr (WIDTH >= 32) v = v + xor_perm<16>(v);
+  if constexpr (WIDTH >= 64) v = swap_add<32>(v, v);
+  if constexpr (WIDTH >= 32) v = swap_add<16>(v, v);
   if constexpr (WIDTH >= 16) v = v + xor_perm<8>(v);
   if constexpr (WIDTH >= 8) v = v + xor_perm<4>(v);
   if constexpr (WIDTH >= 4) v = v + xor_perm<2>(v);
@@ -121,8 +162,8 @@ __device__ __forceinline__ float xor_sum(float v) {
 }
 template <int WIDTH>
 __device__ __forceinline__ int xor_sum_i(int v) {
-  if constexpr (WIDTH >= 64) v = v + xor_perm_i<32>(v);
-  if constexpr (WIDTH >= 32) v = v + xor_perm_i<16>(v);
+  if constexpr (WIDTH >= 64) v = swap_add<32>(v, v);
+  if constexpr (WIDTH >= 32) v = swap_add<16>(v, v);
   if constexpr (WIDTH >= 16) v = v + xor_perm_i<8>(v);
   if constexpr (WIDTH >= 8) v = v + xor_perm_i<4>(v);
   if constexpr (WIDTH >= 4) v = v + xor_perm_i<2>(v);

@@ -373,9 +373,7 @@ int launch_stages(qh_engine* e, const std::vector<Stage>& v, hipStream_t s, hipE
       case ST_ATTN: QH_HIP(launch_attn(st.at, s)); break;
       case ST_COMBINE: QH_HIP(launch_attn_combine(st.at, s)); break;
       default:
-        if (head_t0) QH_HIP(hipEventRecord(head_t0, s));
-        QH_HIP(launch_head(st.hd, e->head_grid, s));
-        if (head_t1) QH_HIP(hipEventRecord(head_t1, s));
+        QH_HIP(launch_head(st.hd, e->head_grid, s, head_t0, head_t1));
         QH_HIP(launch_argmax(e->part_val, e->part_idx, e->head_grid, e->ctl, nullptr, s));
         break;
     }
@@ -816,7 +814,7 @@ int qh_engine_profile(qh_engine* e, int n_steps, float* step_ms, float* head_ms)
   for (int i = 0; st == QH_OK && i < n_steps; ++i) {
     st = hip_status(launch_set_int(&e->ctl->done, 0, s));
     if (st == QH_OK) st = hip_status(hipEventRecord(a, s));
-    if (st == QH_OK) st = enqueue_step(e, false, false, s, h0, h1);
+    if (st == QH_OK) st = enqueue_step(e, false, false, s, h0, h1);   // head events: kernel start / end
     if (st == QH_OK) st = hip_status(hipEventRecord(b, s));
     if (st == QH_OK) st = hip_status(hipEventSynchronize(b));
     float t = 0.0f, th = 0.0f;

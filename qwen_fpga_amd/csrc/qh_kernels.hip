@@ -2,6 +2,8 @@
 // op-level C ABI and the graph engine, over the bodies in qh_stages.hpp, plus
 // the small op kernels.  Every reduction follows the fixed orders documented
 // in qh_device.hpp, so results do not depend on grid size or timing.
+#include <hip/hip_ext.h>
+
 #include "qh_stages.hpp"
 
 namespace qh {
@@ -67,9 +69,14 @@ __global__ __launch_bounds__(256) void head_kernel(const HeadArgs a) {
   head_body(a, blockIdx.x, gridDim.x, io, a.logits);
 }
 
-hipError_t launch_head(const HeadArgs& a, int grid, hipStream_t s) {
-  head_kernel<<<grid, 256, 0, s>>>(a);
-  return hipGetLastError();
+hipError_t launch_head(const HeadArgs& a, int grid, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
+  if (t0 == nullptr && t1 == nullptr) {
+    head_kernel<<<grid, 256, 0, s>>>(a);
+    return hipGetLastError();
+  }
+  // events stamped at the kernel's own start and end (no dispatch gap)
+  void* args[] = {const_cast<HeadArgs*>(&a)};
+  return hipExtLaunchKernel(reinterpret_cast<const void*>(head_kernel), dim3(grid), dim3(256), args, 0, s, t0, t1, 0);
 }
 
 __global__ __launch_bounds__(256) void argmax_kernel(const float* pv, const int* pi, int n, StepCtl* ctl,

@@ -197,7 +197,8 @@ int persist_max_grid(int* grid);   // workgroups the cooperative launch can hold
 
 // ---- launch wrappers (return hipError_t) ----
 hipError_t launch_gemv(const GemvArgs& a, int waves_per_block, hipStream_t s);
-hipError_t launch_head(const HeadArgs& a, int grid, hipStream_t s);
+// t0 / t1 (optional): events stamped at the kernel's own start and end
+hipError_t launch_head(const HeadArgs& a, int grid, hipStream_t s, hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);
 hipError_t launch_argmax(const float* pv, const int* pi, int n, StepCtl* ctl, int* out_idx,
                          hipStream_t s);
 hipError_t launch_deltanet(const DnArgs& a, hipStream_t s);

@@ -2,9 +2,13 @@
 // (qh_kernels.hip: op-level C ABI and the graph engine) and the persistent
 // decode kernel (qh_persist.hip).  Each body runs as
 //
-//   io.arrive()     (no-op hook kept for symmetry with the stage boundary)
-//   prefetch        weights / own state of the first work item in flight
-//   io.wait()       the per-stage kernels check the engine's stop flag here
+//   io.arrive()     the per-stage kernels issue the load of the engine's stop flag
+//   prefetch        input vector, weights / own state of the first work item in flight
+//   io.wait()       the per-stage kernels check the stop flag here
+//
+// A wave's loads return in issue order, so every load whose value is needed
+// first (stop flag, then input vector) is issued before the weights: waiting
+// for it then does not wait for the weights.
 //   compute         vectors produced by other workgroups are read through the
 //                   I/O policy, results are written through it
 //
@@ -66,10 +70,16 @@ struct PlainIO {
   static constexpr bool kTagged = false;
   const int* done = nullptr;   // engine stop flag (graph engine); null: never stopped
   int ring = 0;                // next LDS slot
+  int dv = 0;                  // the stop flag, loaded by arrive()
   __device__ __forceinline__ float* slot() { return lds_ring() + kLdsSlot * (ring++ & 3); }
   __device__ __forceinline__ void mark(int) {}
-  __device__ __forceinline__ void arrive() {}
-  __device__ __forceinline__ bool wait() { return done == nullptr || ldc_i(done) == 0; }
+  // Issued before any weight load of the stage: a wave's loads return in
+  // issue order, so waiting for the flag in wait() then waits for this load
+  // only.  Without a flag the load goes through an empty descriptor (reads 0).
+  __device__ __forceinline__ void arrive() {
+    dv = (int)__builtin_amdgcn_raw_buffer_load_b32(rsrc_n(done, done != nullptr ? 4 : 0), 0, 0, kSc1);
+  }
+  __device__ __forceinline__ bool wait() { return dv == 0; }
   // N chunks of 16 consecutive elements starting at idx[j] (a multiple of 4)
   template <int N>
   __device__ __forceinline__ bool ld16(const float* base, int, const int (&idx)[N], float (&v)[N][16]) {
@@ -115,21 +125,43 @@ struct PlainIO {
   }
   // A vector the workgroup copied to LDS earlier in this stage program (none here).
   __device__ __forceinline__ const float* cached(const float*, int) const { return nullptr; }
-  struct VecPoll {};
-  __device__ __forceinline__ void stage_issue(const float*, int, VecPoll&) {}
-  __device__ __forceinline__ bool stage_finish(const float* base, int st, int K, float* lds, VecPoll&) {
-    return stage_vec(base, st, K, lds);
+  // Workgroup copy of a vector, in two steps around the stage's weight loads:
+  // stage_issue loads elements 4 (t + i blockDim) .. +3 for i < kPL (through a
+  // descriptor over exactly K floats, so loads past the end read 0 and K = 0
+  // loads nothing); stage_finish writes them to LDS, copies whatever a small
+  // workgroup did not cover, and ends with a workgroup barrier.
+  static constexpr int kPL = 4;   // 4 x 16 B per thread: K <= 4096 with 256 threads
+  struct VecPoll {
+    u32x4 u[kPL];
+  };
+  __device__ __forceinline__ void stage_issue(const float* base, int K, VecPoll& vp) {
+    const __amdgpu_buffer_rsrc_t rs = rsrc_n(base, 4 * K);
+#pragma unroll
+    for (int i = 0; i < kPL; ++i)
+      vp.u[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * ((int)threadIdx.x + i * (int)blockDim.x), 0, kSc1);
   }
-  // The whole workgroup copies elements [0, K) (K a multiple of 4) into lds;
-  // every thread must call it (it ends with a workgroup barrier).
-  __device__ __forceinline__ bool stage_vec(const float* base, int, int K, float* lds) {
-    for (int i = 4 * (int)threadIdx.x; i < K; i += 4 * (int)blockDim.x) {
+  __device__ __forceinline__ bool stage_finish(const float*  base, int, int K, float* lds, VecPoll& vp) {
+#pragma unroll
+    for (int i = 0; i < kPL; ++i) {
+      const int p = 4 * ((int)threadIdx.x + i * (int)blockDim.x);
+      if (p < K)
+        *reinterpret_cast<float4*>(lds + p) = make_float4(__uint_as_float(vp.u[i][0]), __uint_as_float(vp.u[i][1]),
+                                                          __uint_as_float(vp.u[i][2]), __uint_as_float(vp.u[i][3]));
+    }
+    for (int p = 4 * ((int)threadIdx.x + kPL * (int)blockDim.x); p < K; p += 4 * (int)blockDim.x) {
       float v[4];
-      ldc4(base, i, v);
-      *reinterpret_cast<float4*>(lds + i) = make_float4(v[0], v[1], v[2], v[3]);
+      ldc4(base, p, v);
+      *reinterpret_cast<float4*>(lds + p) = make_float4(v[0], v[1], v[2], v[3]);
     }
     __syncthreads();
     return true;
+  }
+  // The whole workgroup copies elements [0, K) (K a multiple of 4) into lds;
+  // every thread must call it (it ends with a workgroup barrier).
+  __device__ __forceinline__ bool stage_vec(const float* base, int st, int K, float* lds) {
+    VecPoll vp;
+    stage_issue(base, K, vp);
+    return stage_finish(base, st, K, lds, vp);
   }
 };
 
@@ -410,24 +442,10 @@ struct TagIO {
 // ===========================================================================
 template <typename T>
 __device__ __forceinline__ T reduce8(T v[8], int lane) {
-  {
-    const bool up = (lane & 32) != 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const T send = up ? v[i] : v[i + 4];
-      const T keep = up ? v[i + 4] : v[i];
-      v[i] = keep + xperm<32>(send);
-    }
-  }
-  {
-    const bool up = (lane & 16) != 0;
+  for (int i = 0; i < 4; ++i) v[i] = swap_add<32>(v[i], v[i + 4]);   // lanes with bit 32 keep v[i + 4]
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const T send = up ? v[i] : v[i + 2];
-      const T keep = up ? v[i + 2] : v[i];
-      v[i] = keep + xperm<16>(send);
-    }
-  }
+  for (int i = 0; i < 2; ++i) v[i] = swap_add<16>(v[i], v[i + 2]);   // lanes with bit 16 keep v[i + 2]
   {
     const bool up = (lane & 8) != 0;
     const T send = up ? v[0] : v[1];
@@ -442,22 +460,10 @@ __device__ __forceinline__ T reduce8(T v[8], int lane) {
 }
 
 template <typename T>
-__device__ __forceinline__ T reduce4(T v[4], int lane) {
-  {
-    const bool up = (lane & 32) != 0;
+__device__ __forceinline__ T reduce4(T v[4], int) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const T send = up ? v[i] : v[i + 2];
-      const T keep = up ? v[i + 2] : v[i];
-      v[i] = keep + xperm<32>(send);
-    }
-  }
-  {
-    const bool up = (lane & 16) != 0;
-    const T send = up ? v[0] : v[1];
-    const T keep = up ? v[1] : v[0];
-    v[0] = keep + xperm<16>(send);
-  }
+  for (int i = 0; i < 2; ++i) v[i] = swap_add<32>(v[i], v[i + 2]);
+  v[0] = swap_add<16>(v[0], v[1]);
   T r = v[0];
   r = r + xperm<8>(r);
   r = r + xperm<4>(r);
@@ -467,12 +473,9 @@ __device__ __forceinline__ T reduce4(T v[4], int lane) {
 }
 
 template <typename T>
-__device__ __forceinline__ T reduce2(T v[2], int lane) {
-  const bool up = (lane & 32) != 0;
-  const T send = up ? v[0] : v[1];
-  const T keep = up ? v[1] : v[0];
-  T r = keep + xperm<32>(send);
-  r = r + xperm<16>(r);
+__device__ __forceinline__ T reduce2(T v[2], int) {
+  T r = swap_add<32>(v[0], v[1]);
+  r = swap_add<16>(r, r);
   r = r + xperm<8>(r);
   r = r + xperm<4>(r);
   r = r + xperm<2>(r);
@@ -482,9 +485,8 @@ __device__ __forceinline__ T reduce2(T v[2], int lane) {
 
 template <typename T>
 __device__ __forceinline__ T reduce1(T v[1], int) {
-  T r = v[0];
-  r = r + xperm<32>(r);
-  r = r + xperm<16>(r);
+  T r = swap_add<32>(v[0], v[0]);
+  r = swap_add<16>(r, r);
   r = r + xperm<8>(r);
   r = r + xperm<4>(r);
   r = r + xperm<2>(r);
@@ -885,15 +887,32 @@ __device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
   }
 }
 
-__device__ __forceinline__ void head_load(const HeadArgs& a, int b, int lane, int rl, uint32_t (&w)[8][4], float& sc) {
+// Loads of one batch (8 rows and this lane's row scale).  Every load is issued
+// unconditionally: a batch beyond the last one goes through empty descriptors
+// (no memory access, reads 0), so the loop keeps no conditionally loaded
+// registers and the compiler waits for exactly the batch it consumes.
+__device__ __forceinline__ void head_load(const HeadArgs& a, int b, int total, int lane, int rl, uint32_t (&w)[8][4],
+                                          float& sc) {
+  b = __builtin_amdgcn_readfirstlane(b);   // wave-uniform: scalar descriptors
+  const bool in = b < total;
+  const __amdgpu_buffer_rsrc_t rw = rsrc_n(a.w, in ? 0x7ffffff0 : 0);
+  const __amdgpu_buffer_rsrc_t rs = rsrc_n(a.sw, in ? 0x7ffffff0 : 0);
+  const int bb = in ? b : 0;
 #pragma unroll
-  for (int r = 0; r < 8; ++r) load16b(a.w + (size_t)(b * 8 + r) * 1024 + 16 * lane, w[r]);
-  sc = a.sw[b * 8 + rl];
+  for (int r = 0; r < 8; ++r) {
+    const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rw, (bb * 8 + r) * 1024 + 16 * lane, 0, 0);
+    w[r][0] = t[0];
+    w[r][1] = t[1];
+    w[r][2] = t[2];
+    w[r][3] = t[3];
+  }
+  sc = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (bb * 8 + rl) * 4, 0, 0));
 }
 
 template <class IO>
 __device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, IO& io, float* logits) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwv = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, nwv = blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int total = a.rows / kRowsPerBatch;
   const int stride = nblk * nwv;
   int b = blk * nwv + wave;
@@ -903,8 +922,8 @@ __device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, 
   io.stage_issue(a.h, 1024, vh);
   uint32_t w0[8][4], w1[8][4];
   float sc0 = 0.0f, sc1 = 0.0f;
-  if (b < total) head_load(a, b, lane, rl, w0, sc0);   // two batches in flight before the norm prologue
-  if (b + stride < total) head_load(a, b + stride, lane, rl, w1, sc1);
+  head_load(a, b, total, lane, rl, w0, sc0);   // two batches in flight before the norm prologue
+  head_load(a, b + stride, total, lane, rl, w1, sc1);
   float xv[16], nw[16];
   load16f(a.nw + 16 * lane, nw);
   if (!io.wait()) return false;
@@ -920,36 +939,29 @@ __device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, 
   for (int e = 0; e < 16; ++e) xv[e] = (xv[e] * inv) * (1.0f + nw[e]);
   float bv = -1e30f;
   int bi = 0;
-  for (; b < total; b += 2 * stride) {
-    {   // batch b (w0); its slot is refilled with batch b + 2 stride before the reduction
-      float p[8];
+  // batch bb from buffer (w, sc); the buffer is refilled with batch bb + 2 stride
+  // before the reduction.  Both halves of the loop body run unconditionally (a
+  // wave with an odd number of batches finishes in the tail), so the buffers
+  // keep fixed registers and each wait covers exactly the batch consumed.
+  auto batch = [&](int bb, uint32_t (&w)[8][4], float& sc) {
+    float p[8];
 #pragma unroll
-      for (int r = 0; r < 8; ++r) p[r] = dot16_i8f(w0[r], xv, 0.0f);
-      const float scur = sc0;
-      if (b + 2 * stride < total) head_load(a, b + 2 * stride, lane, rl, w0, sc0);
-      const float y = reduce8(p, lane) * scur;
-      const int row = b * 8 + rl;
-      if ((lane & 7) == 0) {
-        if (logits != nullptr) logits[row] = y;
-        better(bv, bi, y, row);
-      }
+    for (int r = 0; r < 8; ++r) p[r] = dot16_i8f(w[r], xv, 0.0f);
+    float scur;   // an explicit copy frees sc's register for the next load (no copy at the loop latch)
+    asm volatile("v_mov_b32 %0, %1" : "=v"(scur) : "v"(sc));
+    head_load(a, bb + 2 * stride, total, lane, rl, w, sc);
+    const float y = reduce8(p, lane) * scur;
+    const int row = bb * 8 + rl;
+    if ((lane & 7) == 0) {
+      if (logits != nullptr) logits[row] = y;
+      better(bv, bi, y, row);
     }
-    const int b1 = b + stride;
-    if (b1 >= total) break;
-    {   // batch b + stride (w1)
-      float p[8];
-#pragma unroll
-      for (int r = 0; r < 8; ++r) p[r] = dot16_i8f(w1[r], xv, 0.0f);
-      const float scur = sc1;
-      if (b1 + 2 * stride < total) head_load(a, b1 + 2 * stride, lane, rl, w1, sc1);
-      const float y = reduce8(p, lane) * scur;
-      const int row = b1 * 8 + rl;
-      if ((lane & 7) == 0) {
-        if (logits != nullptr) logits[row] = y;
-        better(bv, bi, y, row);
-      }
-    }
+  };
+  for (; b + stride < total; b += 2 * stride) {
+    batch(b, w0, sc0);
+    batch(b + stride, w1, sc1);
   }
+  if (b < total) batch(b, w0, sc0);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     const float ov = __shfl_xor(bv, off, 64);
