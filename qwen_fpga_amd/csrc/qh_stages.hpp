@@ -674,6 +674,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
   int b = blk * nwv + wave;
 
   io.arrive();
+  io.mark(0);   // trace: stage entry
   if (blk * nwv >= total) return true;   // no rows for this workgroup (workgroup-uniform)
   // ---------------- 1. the first poll of x, then weights and epilogue inputs of the first batch
   // One straight-line block issues every load of the first batch: the first
@@ -714,6 +715,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
     if (!io.stage_vec(a.z, a.z_st, K, buf)) return false;
     zl = buf;
   }
+  io.mark(1);   // trace: input vector in LDS
   if (b >= total) return true;   // no rows for this wave (block 0 / wave 0 always has some)
 
   // ---------------- 2. prologue: this lane's chunks c = lane + 64 j of x
@@ -806,6 +808,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
     }
   }
 
+  io.mark(2);   // trace: prologue done
   // ---------------- 3. row batches (the next batch's loads overlap this batch's reduction)
   for (; b < total; b += stride) {
     const Seg& g = a.seg[si];
