@@ -17,10 +17,22 @@
 
 namespace qh {
 
+// The stage bodies read their descriptors from a workgroup copy in LDS: read
+// from the program in global memory, every descriptor field would be a vector
+// load whose wait also waits for every load and store issued before it.  The
+// copy of stage i + 1 is loaded (one word per thread) at the start of stage i,
+// ahead of that stage's own loads, and written to the other of two LDS slots
+// at the start of stage i + 1, followed by one workgroup barrier.  A slot is
+// rewritten two stages after it was filled; every wave has passed the barrier
+// of the stage in between, so no wave still reads it.
+constexpr int kStageWords = (int)(sizeof(Stage) / 4);
+static_assert(sizeof(Stage) % 4 == 0 && kStageWords <= kPersistThreads, "one descriptor word per thread");
+
 template <int MODE>
 __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistArgs P) {
   __shared__ float s_bv[kPersistThreads / 64];
   __shared__ int s_bi[kPersistThreads / 64];
+  __shared__ __attribute__((aligned(16))) uint32_t s_stage[2][kStageWords];
   const int blk = blockIdx.x, nblk = gridDim.x;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   TagIO io;
@@ -32,10 +44,19 @@ __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistA
   int argmax = P.ctl->argmax, done = 0, err = 0, aborted = 0;
   const HeadArgs& hd = P.prog[P.nstage - 1].hd;
 
+  const uint32_t* progw = reinterpret_cast<const uint32_t*>(P.prog);
+  uint32_t nxt = t < kStageWords ? progw[t] : 0u;   // descriptor word of stage 0
+  int slot = 0;
   for (int k = 0;; ++k) {
     io.tag0 = P.tag_base + (uint32_t)k * (uint32_t)kTagsPerToken;
     for (int i = 0; i < P.nstage; ++i) {
-      const Stage& st = P.prog[i];
+      if (t < kStageWords) s_stage[slot][t] = nxt;
+      __syncthreads();
+      const Stage& st = *reinterpret_cast<const Stage*>(s_stage[slot]);
+      slot ^= 1;
+      const int ni = i + 1 < P.nstage ? i + 1 : 0;   // the next stage (stage 0 after the head)
+      nxt = t < kStageWords ? progw[(size_t)ni * kStageWords + t] : 0u;
+      asm volatile("" ::: "memory");   // issued before any load of this stage
       uint64_t* tr = (P.trace != nullptr && k < P.trace_tokens) ? P.trace + (((size_t)k * P.nstage + i) * nblk + blk) * 4 : nullptr;
       io.tr = tr;
       bool ok;
