@@ -218,6 +218,11 @@ int qh_generate(qh_engine* e, const int* prompt, int n_prompt, int n_new, int eo
 int qh_engine_pos(const qh_engine* e);
 /* Argmax of the most recent completed step (the next greedy token). */
 int qh_engine_last_argmax(const qh_engine* e);
+/* Duration (ms) of the last persistent-kernel launch, from HIP events recorded
+ * on the engine stream right before and after the cooperative launch (0 before
+ * the first persistent launch).  Measurement hook; no counterpart in the
+ * reference. */
+float qh_engine_last_launch_ms(const qh_engine* e);
 /* Run layers [l0, l1) of one decode step on a device hidden vector h (in place,
  * [1024]) without embed / final norm / head; state and pos advance as in a
  * full step.  Used for the 4-layer block configuration. */

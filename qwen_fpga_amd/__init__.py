@@ -105,6 +105,8 @@ def _lib() -> ctypes.CDLL:
         lib.qh_synth_fill_i8.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint64]
         lib.qh_engine_stream.restype = ctypes.c_void_p
         lib.qh_engine_stream.argtypes = [ctypes.c_void_p]
+        lib.qh_engine_last_launch_ms.restype = ctypes.c_float
+        lib.qh_engine_last_launch_ms.argtypes = [ctypes.c_void_p]
         lib.qh_engine_device_ptr.restype = ctypes.c_void_p
         lib.qh_engine_device_ptr.argtypes = [ctypes.c_void_p, ctypes.c_int]
         _LIB = lib
@@ -415,3 +417,8 @@ class Engine:
     @property
     def last_argmax(self) -> int:
         return int(_lib().qh_engine_last_argmax(self._h))
+
+    @property
+    def last_launch_ms(self) -> float:
+        """Duration of the last persistent-kernel launch (HIP events on the engine stream)."""
+        return float(_lib().qh_engine_last_launch_ms(self._h))

@@ -69,6 +69,8 @@ struct qh_engine {
   size_t arena_pairs = 0;
   uint32_t tag_next = 1;         // first unused tag (the arena holds only smaller tags)
   int* abort_dev = nullptr;      // set by a hand-over wait that gave up
+  hipEvent_t launch_ev[2] = {};  // around the last persistent launch (engine stream)
+  float last_launch_ms = 0.0f;
 };
 
 namespace {
@@ -468,6 +470,7 @@ int run_persist(qh_engine* e, int tok0, int n_prompt, int n_new, int eos, bool w
   a.out_ids = e->out_dev;
   a.logits = with_logits ? e->logits : nullptr;
   a.abort_flag = e->abort_dev;
+  QH_HIP(hipEventRecord(e->launch_ev[0], s));
   if (launch_persist(a, e->persist_grid, s) != hipSuccess) {
     (void)hipGetLastError();
     if (trace != nullptr) (void)hipFree(trace);
@@ -475,6 +478,7 @@ int run_persist(qh_engine* e, int tok0, int n_prompt, int n_new, int eos, bool w
     e->exec = QH_EXEC_GRAPH;
     return kUseGraph;
   }
+  QH_HIP(hipEventRecord(e->launch_ev[1], s));
   e->tag_next += (uint32_t)need;
   int aborted = 0;
   QH_HIP(hipMemcpyAsync(out, e->ctl, sizeof *out, hipMemcpyDeviceToHost, s));
@@ -501,6 +505,7 @@ int run_persist(qh_engine* e, int tok0, int n_prompt, int n_new, int eos, bool w
       std::fclose(f);
     }
   }
+  QH_HIP(hipEventElapsedTime(&e->last_launch_ms, e->launch_ev[0], e->launch_ev[1]));
   e->host_pos = out->pos;
   e->last_argmax = out->argmax;
   if (out->err == 3 || aborted != 0) return QH_EDEVICE;
@@ -554,6 +559,8 @@ void release(qh_engine* e) {
                   e->abort_dev};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
+  for (hipEvent_t ev : e->launch_ev)
+    if (ev) (void)hipEventDestroy(ev);
   if (e->stream) (void)hipStreamDestroy(e->stream);
   delete e;
 }
@@ -622,6 +629,8 @@ int create(const void* blob, size_t blob_len, const char* idx_text, int max_ctx,
   QH_C(dalloc(&e->abort_dev, 1));
   if (persist_max_grid(&e->persist_grid) != 0) e->persist_grid = 0;
   if (e->persist_grid == 0) e->exec = QH_EXEC_GRAPH;
+  QH_C(hip_status(hipEventCreate(&e->launch_ev[0])));
+  QH_C(hip_status(hipEventCreate(&e->launch_ev[1])));
   QH_C(dalloc(&e->ctl, 1));
   {
     std::vector<float> rope((size_t)max_ctx * 64);
@@ -785,6 +794,7 @@ int qh_generate(qh_engine* e, const int* prompt, int n_prompt, int n_new, int eo
 
 int qh_engine_pos(const qh_engine* e) { return e ? e->host_pos : -1; }
 int qh_engine_last_argmax(const qh_engine* e) { return e ? e->last_argmax : -1; }
+float qh_engine_last_launch_ms(const qh_engine* e) { return e ? e->last_launch_ms : 0.0f; }
 
 int qh_engine_forward_layers(qh_engine* e, int l0, int l1, float* h) {
   if (!e || !h || l0 < 0 || l1 > kLayers || l0 >= l1) return QH_EINVAL;
