@@ -243,8 +243,22 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
 // pointer must be the same on every lane of the wave.  Weights and state that
 // one workgroup owns use ordinary accesses.
 constexpr int kSc1 = 16;   // cache-policy operand: sc1
+
+// A buffer descriptor sits in scalar registers.  Every base address that
+// builds one here is the same on all lanes of the wave (a kernel argument or a
+// stage-descriptor field that every lane reads from the same LDS word), but a
+// value read from LDS lands in a vector register and the compiler cannot see
+// that it is uniform: it would wrap each access in a loop over the distinct
+// values.  readfirstlane states the uniformity, so an access is one
+// instruction.  Callers must pass wave-uniform values.
+__device__ __forceinline__ void* wave_uniform(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+}
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t coh_rsrc(const void* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7ffffff0, 0x00020000);
+  return __builtin_amdgcn_make_buffer_rsrc(wave_uniform(base), (short)0, 0x7ffffff0, 0x00020000);
 }
 __device__ __forceinline__ float ldc(const float* p) {
   return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,

@@ -454,7 +454,7 @@ int run_persist(qh_engine* e, int tok0, int n_prompt, int n_new, int eos, bool w
   const char* trace_path = std::getenv("QH_TRACE_FILE");
   uint64_t* trace = nullptr;
   const int trace_tokens = 2;
-  const size_t trace_n = (size_t)trace_tokens * e->prog_n * e->persist_grid * 4;
+  const size_t trace_n = (size_t)trace_tokens * e->prog_n * e->persist_grid * kTraceSlots;
   if (trace_path != nullptr && trace_path[0] != '\0') {
     QH_TRY(dalloc(&trace, trace_n));
     QH_HIP(hipMemsetAsync(trace, 0, sizeof(uint64_t) * trace_n, s));
@@ -490,7 +490,8 @@ int run_persist(qh_engine* e, int tok0, int n_prompt, int n_new, int eos, bool w
     (void)hipFree(trace);
     QH_HIP(ce);
     if (FILE* f = std::fopen(trace_path, "w")) {
-      std::fprintf(f, "# token stage block t0 t1 t2 done (s_memrealtime ticks; 0 = not reached); %d stages per token, kinds:", e->prog_n);
+      std::fprintf(f, "# token stage block m0..m%d done (s_memrealtime ticks; 0 = not reached); %d stages per token, kinds:",
+                   kTraceSlots - 2, e->prog_n);
       std::vector<Stage> kinds(e->prog_n);
       if (hipMemcpy(kinds.data(), e->prog[e->mode], sizeof(Stage) * e->prog_n, hipMemcpyDeviceToHost) == hipSuccess)
         for (const Stage& k : kinds) std::fprintf(f, " %d", k.kind);
@@ -498,9 +499,10 @@ int run_persist(qh_engine* e, int tok0, int n_prompt, int n_new, int eos, bool w
       for (int k = 0; k < trace_tokens; ++k)
         for (int i = 0; i < e->prog_n; ++i)
           for (int b = 0; b < e->persist_grid; ++b) {
-            const uint64_t* q = &hbuf[(((size_t)k * e->prog_n + i) * e->persist_grid + b) * 4];
-            std::fprintf(f, "%d %d %d %llu %llu %llu %llu\n", k, i, b, (unsigned long long)q[0],
-                         (unsigned long long)q[1], (unsigned long long)q[2], (unsigned long long)q[3]);
+            const uint64_t* q = &hbuf[(((size_t)k * e->prog_n + i) * e->persist_grid + b) * kTraceSlots];
+            std::fprintf(f, "%d %d %d", k, i, b);
+            for (int m = 0; m < kTraceSlots; ++m) std::fprintf(f, " %llu", (unsigned long long)q[m]);
+            std::fprintf(f, "\n");
           }
       std::fclose(f);
     }

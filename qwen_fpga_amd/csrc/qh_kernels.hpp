@@ -187,10 +187,11 @@ struct PersistArgs {
   int* out_ids = nullptr;       // [n_new]
   float* logits = nullptr;      // optional: logits of every step (the last one remains)
   int* abort_flag = nullptr;    // set when a hand-over wait exceeds its poll limit
-  uint64_t* trace = nullptr;    // optional [trace_tokens][nstage][grid]: completion time of each stage
+  uint64_t* trace = nullptr;    // optional [trace_tokens][nstage][grid][kTraceSlots]: stage marks and end
   int trace_tokens = 0;
 };
 constexpr int kPersistThreads = 256;
+constexpr int kTraceSlots = 8;  // marks 0..6 of a stage body, then its completion time
 
 hipError_t launch_persist(const PersistArgs& a, int grid, hipStream_t s);
 int persist_max_grid(int* grid);   // workgroups the cooperative launch can hold (a multiple of 16)

@@ -57,7 +57,7 @@ __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistA
       const int ni = i + 1 < P.nstage ? i + 1 : 0;   // the next stage (stage 0 after the head)
       nxt = t < kStageWords ? progw[(size_t)ni * kStageWords + t] : 0u;
       asm volatile("" ::: "memory");   // issued before any load of this stage
-      uint64_t* tr = (P.trace != nullptr && k < P.trace_tokens) ? P.trace + (((size_t)k * P.nstage + i) * nblk + blk) * 4 : nullptr;
+      uint64_t* tr = (P.trace != nullptr && k < P.trace_tokens) ? P.trace + (((size_t)k * P.nstage + i) * nblk + blk) * kTraceSlots : nullptr;
       io.tr = tr;
       bool ok;
       switch (st.kind) {
@@ -70,7 +70,7 @@ __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistA
         case ST_COMBINE: ok = combine_body(st.at, pos, blk, io); break;
         default: ok = head_body(st.hd, blk, nblk, io, P.logits); break;
       }
-      if (tr != nullptr && t == 0) tr[3] = __builtin_amdgcn_s_memrealtime();
+      if (tr != nullptr && t == 0) tr[kTraceSlots - 1] = __builtin_amdgcn_s_memrealtime();
       if (!ok) {
         aborted = 1;
         break;

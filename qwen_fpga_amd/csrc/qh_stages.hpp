@@ -50,9 +50,11 @@ struct Raw {
 __device__ __forceinline__ bool wave_all(bool ok) { return __builtin_amdgcn_ballot_w64(!ok) == 0; }
 
 // Buffer descriptor over n bytes at base; n = 0 makes every access a no-op
-// that reads 0, so optional loads can be issued without a branch.
+// that reads 0, so optional loads can be issued without a branch.  base and n
+// must be wave-uniform (scalar registers; see wave_uniform).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_n(const void* base, int n) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+  return __builtin_amdgcn_make_buffer_rsrc(wave_uniform(base), (short)0, __builtin_amdgcn_readfirstlane(n),
+                                           0x00020000);
 }
 
 // Workgroup copies of handed-over vectors (GEMV inputs, the LM head's h): a
@@ -389,7 +391,9 @@ struct TagIO {
   __device__ __forceinline__ bool stage_finish(const float* base, int st, int K, float* lds, VecPoll& vp) {
     const uint32_t tg = tag(st);
     const int t = threadIdx.x, lane = t & 63;
-    if (!vec_tags(vp, K, tg)) {
+    const bool hit = vec_tags(vp, K, tg);
+    mark(3);   // trace: first poll returned
+    if (!hit) {
       const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
       // 16 sampled lines per wave (lanes in groups of 4 share one), rotated per
       // workgroup so that the waiting workgroups spread their polls over the
@@ -401,6 +405,7 @@ struct TagIO {
         if (!again(polls) || !sample(rs, (int)(2 * sidx + 1), tg, polls)) return false;
         stage_issue(base, K, vp);
       } while (!vec_tags(vp, K, tg));
+      mark(4);   // trace: vector complete after a repoll
     }
 #pragma unroll
     for (int i = 0; i < kL; ++i) {
@@ -558,10 +563,13 @@ __device__ __forceinline__ void epi_prefetch(const Seg& g, int myrow, EpiAux& x,
   constexpr int kBig = 0x7ffffff0;
   const int r = min(myrow, g.rows - 1);   // always a valid address; unused rows are never stored
   const bool pair = g.kind == SEG_PAIR;
-  const float* swp = (pair && (r & 1)) ? g.sw2 : g.sw;
-  const float sc = __uint_as_float(
-      __builtin_amdgcn_raw_buffer_load_b32(rsrc_n(swp, g.kind == SEG_F32 ? 0 : kBig), (pair ? (r >> 1) : r) * 4, 0, 0));
-  x.sc = g.kind == SEG_F32 ? 1.0f : sc;
+  // the row's scale: lanes of a pair segment take even rows (gate) from sw and
+  // odd rows (up) from sw2, so both are loaded through uniform descriptors
+  const int i8n = g.kind == SEG_F32 ? 0 : kBig;
+  const int si = (pair ? (r >> 1) : r) * 4;
+  const float sa = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_n(g.sw, i8n), si, 0, 0));
+  const float sb = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_n(g.sw2, pair ? kBig : 0), si, 0, 0));
+  x.sc = g.kind == SEG_F32 ? 1.0f : ((pair && (r & 1)) ? sb : sa);
   x.res = io.issue1(g.res, r, g.epi == E_RESID);   // residual: written by another workgroup
   const bool ga = g.epi == E_GATE_A, cv = g.epi == E_CONV;
   const float a_log = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_n(g.c0, ga ? kBig : 0), r * 4, 0, 0));
@@ -636,18 +644,17 @@ __device__ __forceinline__ void load_batch(const Seg& g, int row0, int K, int nc
                                            uint32_t (&w)[NCH][R][4]) {
   const bool pair = g.kind == SEG_PAIR;
   const int n = g.kind == SEG_F32 ? 0 : 0x7ffffff0;
-  const __amdgpu_buffer_rsrc_t ra = rsrc_n(g.w, n);
-  const __amdgpu_buffer_rsrc_t rb = rsrc_n(pair ? g.w2 : g.w, n);
   const int last = g.rows - 1;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int row = min(row0 + r, last);   // wave-uniform
+    const int row = __builtin_amdgcn_readfirstlane(min(row0 + r, last));   // wave-uniform
     const bool second = pair && (row & 1);
+    const __amdgpu_buffer_rsrc_t rw = rsrc_n(second ? g.w2 : g.w, n);
     const int roff = (pair ? (row >> 1) : row) * K;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int c = min(lane + 64 * j, nchunk - 1);
-      const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(second ? rb : ra, roff + 16 * c, 0, 0);
+      const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rw, roff + 16 * c, 0, 0);
       w[j][r][0] = t[0];
       w[j][r][1] = t[1];
       w[j][r][2] = t[2];
@@ -809,6 +816,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
   }
 
   io.mark(2);   // trace: prologue done
+  const int b0 = b;
   // ---------------- 3. row batches (the next batch's loads overlap this batch's reduction)
   for (; b < total; b += stride) {
     const Seg& g = a.seg[si];
@@ -851,6 +859,15 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
 #pragma unroll
         for (int r = 0; r < R; ++r) pi[r] = dot16_i8i8(w[j][r], xq[j], pi[r]);
     }
+    if (b == b0) {   // trace: dot products of the first batch done (its weights arrived)
+      if constexpr (MODE == M_W8A8) {
+        if (g.kind != SEG_F32) asm volatile("" ::"v"(pi[0]));
+        else asm volatile("" ::"v"(pf[0]));
+      } else {
+        asm volatile("" ::"v"(pf[0]));
+      }
+      io.mark(5);
+    }
     // issue the next batch's loads before reducing this one
     const int bn = b + stride;
     int sin = si;
@@ -871,6 +888,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
     }
     if (g.epi == E_RESID && !io.resolve1(aux.res, g.res, g.res_st, min(myrow, g.rows - 1), aux.a0)) return false;
     gemv_epilogue<R>(g, a.out_st, lane, myrow, y, acci, aux, io);
+    if (b == b0) io.mark(6);   // trace: first batch stored
     si = sin;
     aux = auxn;
   }
@@ -1060,6 +1078,7 @@ __device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool va
   float* Sh = a.S + (size_t)h * 128 * 128;
   __shared__ float gbs[2];
   io.arrive();
+  io.mark(0);   // trace: stage entry
   float s[16];
   bool ok = true;
   if (valid) {
@@ -1096,6 +1115,7 @@ __device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool va
 #pragma unroll
     for (int e = 0; e < 16; ++e) qk[e] = t1[0][e];
   }
+  io.mark(1);   // trace: q, k, v of the head received
   if (wave < 2) {
     float x[16];
     float ss = 0.0f;
@@ -1141,6 +1161,7 @@ __device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool va
     dl[vl] = (vv - pp[0]) * beta;
   }
   __syncthreads();
+  io.mark(2);   // trace: delta computed (sweep A done)
   const float d = dl[vl];
   p = 0.0f;
 #pragma unroll
@@ -1287,6 +1308,7 @@ __device__ __forceinline__ bool attn_unit(const AttnArgs& a, int s, int j, int T
     for (int i = 0; i < 4; ++i) idx[i] = (4 * j + i) * 512 + 16 * g16;
     if (!io.template ld16<4>(a.qkv, a.qkv_st, idx, q)) return false;
   }
+  io.mark(1);   // trace: q (and the new k, v) received
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // constants and V rows of this wave are in LDS
   __syncthreads();
   const float* cl = attn_clds();
@@ -1338,6 +1360,7 @@ __device__ __forceinline__ bool attn_unit(const AttnArgs& a, int s, int j, int T
     }
   }
   __syncthreads();
+  io.mark(2);   // trace: softmax of the split done
   {   // thread t = dimension; position order (attention.hpp:80-86)
     const int cnt = min(kAttnSplit, Tn - t0);
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1364,6 +1387,7 @@ __device__ __forceinline__ bool attn_body(const AttnArgs& a, int T, int blk, int
   const int units = ok ? 2 * ((T + 1 + kAttnSplit - 1) / kAttnSplit) : 0;
   io.arrive();
   if (blk >= units) return true;
+  io.mark(0);   // trace: stage entry
   const int rrow = a.rope_row != nullptr ? ldc_i(a.rope_row) : T;
   AttnPre pf;
   attn_prefetch(a, blk >> 1, blk & 1, T, rrow, pf);
@@ -1380,6 +1404,7 @@ constexpr int kCombineChunk = 8;
 template <class IO>
 __device__ __forceinline__ bool combine_body(const AttnArgs& a, int T, int blk, IO& io) {
   io.arrive();
+  io.mark(0);   // trace: stage entry
   if (!io.wait()) return false;
   const int h = blk, d = threadIdx.x;
   if (h >= 8 || T < 0 || T >= a.max_ctx) return true;
@@ -1417,6 +1442,7 @@ __device__ __forceinline__ bool combine_body(const AttnArgs& a, int T, int blk, 
       }
     }
   }
+  io.mark(1);   // trace: all split partials received
   const float invL = 1.0f / L;
   float gate;
   if (!io.ld1(a.qkv, a.qkv_st, h * 512 + 256 + d, gate)) return false;
