@@ -37,7 +37,7 @@
 #define N_LINEAR 18
 #define N_FULL 6
 /* device-order constants: attention positions per split, DeltaNet k-groups */
-#define DEV_ATTN_SPLIT 64
+#define DEV_ATTN_SPLIT 16
 #define DEV_DN_KGROUPS 8
 
 static int is_linear(int layer) { return (layer % 4) != 3; }   /* types.hpp:47 */

@@ -7,7 +7,7 @@
 namespace qh {
 
 constexpr int kRowsPerBatch = 8;     // rows one wave reduces together (LM head, large GEMVs)
-constexpr int kAttnSplit = 64;       // positions per attention split
+constexpr int kAttnSplit = 16;       // positions per attention split
 constexpr int kDnVQuarters = 4;      // DeltaNet workgroups per head (32 v columns each)
 
 enum SegKind : int { SEG_I8 = 0, SEG_F32 = 1, SEG_PAIR = 2 };

@@ -117,13 +117,24 @@ struct PlainIO {
     stcb(reinterpret_cast<float*>(base), idx, __int_as_float(v));
   }
   __device__ __forceinline__ void st16(float* base, int, int idx, const float* v) { stc16(base, idx, v); }
-  // N 16-element chunks and one more element, all from one vector
+  __device__ __forceinline__ void st4(float* base, int, int idx, const float* v) { stc4(base, idx, v); }
+  // N 16-element chunks and M single elements, all from one vector
+  template <int N, int M>
+  __device__ __forceinline__ bool ld16vn(const float* base, int st, const int (&idx)[N], float (&v)[N][16],
+                                         const int (&idx1)[M], float (&v1)[M]) {
+    ld16<N>(base, st, idx, v);
+#pragma unroll
+    for (int m = 0; m < M; ++m) v1[m] = ldcb(base, idx1[m]);
+    return true;
+  }
   template <int N>
   __device__ __forceinline__ bool ld16v(const float* base, int st, const int (&idx)[N], float (&v)[N][16], int idx1,
                                         float& v1) {
-    ld16<N>(base, st, idx, v);
-    v1 = ldcb(base, idx1);
-    return true;
+    const int i1[1] = {idx1};
+    float o1[1];
+    const bool ok = ld16vn<N, 1>(base, st, idx, v, i1, o1);
+    v1 = o1[0];
+    return ok;
   }
   // A vector the workgroup copied to LDS earlier in this stage program (none here).
   __device__ __forceinline__ const float* cached(const float*, int) const { return nullptr; }
@@ -313,23 +324,29 @@ struct TagIO {
   __device__ __forceinline__ void st1i(int* base, int st, int idx, int v) {
     st1(reinterpret_cast<float*>(base), st, idx, __int_as_float(v));
   }
-  template <int N>
-  __device__ __forceinline__ bool ld16v(const float* base, int st, const int (&idx)[N], float (&v)[N][16], int idx1,
-                                        float& v1) {
+  template <int N, int M>
+  __device__ __forceinline__ bool ld16vn(const float* base, int st, const int (&idx)[N], float (&v)[N][16],
+                                         const int (&idx1)[M], float (&v1)[M]) {
     const uint32_t tg = tag(st);
     const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
     u32x4 u[N][8];
-    u32x2 u1;
+    u32x2 u1[M];
     auto issue = [&]() {
       issue16<N>(rs, idx, u);
-      u1 = __builtin_amdgcn_raw_buffer_load_b64(rs, idx1 * 8, 0, kSc1);
+#pragma unroll
+      for (int m = 0; m < M; ++m) u1[m] = __builtin_amdgcn_raw_buffer_load_b64(rs, idx1[m] * 8, 0, kSc1);
     };
-    auto tags = [&]() { return tags16<N>(u, tg) & wave_all(u1[1] == tg); };
+    auto tags = [&]() {
+      bool ok = true;
+#pragma unroll
+      for (int m = 0; m < M; ++m) ok = ok & (u1[m][1] == tg);
+      return tags16<N>(u, tg) && wave_all(ok);
+    };
     issue();
     if (!tags()) {
       unsigned polls = 0;
       do {
-        if (!again(polls) || !sample(rs, idx1, tg, polls)) return false;
+        if (!again(polls) || !sample(rs, idx1[M - 1], tg, polls)) return false;
         issue();
       } while (!tags());
     }
@@ -340,8 +357,18 @@ struct TagIO {
         v[j][2 * k] = __uint_as_float(u[j][k][0]);
         v[j][2 * k + 1] = __uint_as_float(u[j][k][2]);
       }
-    v1 = __uint_as_float(u1[0]);
+#pragma unroll
+    for (int m = 0; m < M; ++m) v1[m] = __uint_as_float(u1[m][0]);
     return true;
+  }
+  template <int N>
+  __device__ __forceinline__ bool ld16v(const float* base, int st, const int (&idx)[N], float (&v)[N][16], int idx1,
+                                        float& v1) {
+    const int i1[1] = {idx1};
+    float o1[1];
+    const bool ok = ld16vn<N, 1>(base, st, idx, v, i1, o1);
+    v1 = o1[0];
+    return ok;
   }
   // The last vector this workgroup copied to LDS (stage_finish), if it is (base, st).
   const float* last_base = nullptr;
@@ -417,6 +444,20 @@ struct TagIO {
     last_st = st;
     last_lds = lds;
     return true;
+  }
+  // base[idx .. idx + 3], idx even: two (value, tag) pairs per 16-byte store
+  __device__ __forceinline__ void st4(float* base, int st, int idx, const float* v) {
+    const uint32_t tg = tag(st);
+    const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      u32x4 u;
+      u[0] = __float_as_uint(v[2 * k]);
+      u[1] = tg;
+      u[2] = __float_as_uint(v[2 * k + 1]);
+      u[3] = tg;
+      __builtin_amdgcn_raw_buffer_store_b128(u, rs, (idx + 2 * k) * 8, 0, kSc1);
+    }
   }
   __device__ __forceinline__ void st16(float* base, int st, int idx, const float* v) {
     const uint32_t tg = tag(st);
@@ -1199,59 +1240,68 @@ __device__ __forceinline__ bool deltanet_all(const DnArgs& a, int blk, int nblk,
 
 // ===========================================================================
 // Gated GQA attention, split-K flash decoding (attention.hpp:25-95).
-// Unit u = 2 s + j covers positions [64 s, 64 s + 64) of kv head j for the
-// four query heads 4j..4j+3 (GQA kv = h/4).  Before its inputs are ready a unit
-// loads every cached K and V row of its split (positions < T): K in the C16
-// layout (16 lanes x 16 dims, four positions per wave iteration), V as one
-// dimension per thread.  Each wave then normalises and rotates the four
-// queries (QK-norm with (1+w), RoPE on dims 0..63); the unit whose split holds
-// slot T normalises and rotates the new K row itself, takes the new V row, and
-// writes both to the cache.  Scores are C16 dots scaled by 1/16; per head the
-// split max m, p = exp(s - m), the 64-lane tree sum l and the position-ordered
-// fma sum acc = sum p v are written for the combine step.  A split's cache rows
-// are written and read by the same unit.
+// Unit u = 2 s + j covers positions [16 s, 16 s + 16) of kv head j; wave i of
+// the unit handles query head 4 j + i (GQA kv = h/4) on its own, so a unit
+// needs no workgroup barrier and no LDS.  Before its inputs are ready a wave
+// loads the split's cached K rows in the C16 layout (16 lanes x 16 dims, the
+// four lane groups hold four positions, four rows each), the cached V rows
+// with four dimensions per lane, the norm gains and this position's RoPE
+// row.  The cache rows of a split are written (by the unit whose split holds
+// the new slot) and read only by the same unit -- the same workgroup in the
+// persistent kernel, for every token -- so they are read with ordinary loads.
+// After the hand-over the wave normalises and rotates its query (QK-norm with
+// (1+w), RoPE on dims 0..63); in the unit whose split holds slot T every wave
+// also normalises and rotates the new K row and takes the new V elements, and
+// wave 0 writes both to the cache.  Scores are C16 dots scaled by 1/16; per
+// head the split max m, p = exp(s - m), the position-tree sum l of p and the
+// position-ordered fma sum acc = sum p v are written for the combine step.
 // ===========================================================================
-// Everything a unit can load before its inputs are ready: the cached K rows of
-// split s (positions < T) in the C16 layout, the q/k norm gains and this
-// position's RoPE row in registers; the cached V rows go straight to LDS
-// (global_load_lds_dwordx4, no registers), row i of the split at vl + 256 i.
 struct AttnPre {
-  float kreg[4][16];
+  float k[4][16];            // K row of position t0 + 4 it + pg, dims 16 g16 .. +15
+  float v[kAttnSplit][4];    // V row of position t0 + u, dims 4 lane .. +3
+  float qn[16], kn[16];      // q_norm / k_norm gains of dims 16 g16 .. +15
+  float cs[16], sn[16];      // RoPE cos / sin[(16 g16 + e) & 31] (rope.hpp:30-41)
 };
-__device__ __forceinline__ float* attn_vlds() {
-  __shared__ float vl[kAttnSplit * 256];
-  return vl;
+
+__device__ __forceinline__ void load16_rs(const __amdgpu_buffer_rsrc_t& rs, int byte_off, float* v) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rs, byte_off + 16 * k, 0, 0);
+    v[4 * k + 0] = __uint_as_float(t[0]);
+    v[4 * k + 1] = __uint_as_float(t[1]);
+    v[4 * k + 2] = __uint_as_float(t[2]);
+    v[4 * k + 3] = __uint_as_float(t[3]);
+  }
 }
-// q_norm gain [256], k_norm gain [256], RoPE row [64] (cos[32], sin[32])
-__device__ __forceinline__ float* attn_clds() {
-  __shared__ float c[256 + 256 + 64];
-  return c;
-}
+
+// Straight-line loads, no branch: rows at or past slot T are clamped to row
+// T - 1 (T = 0: an empty descriptor, reads 0).  Such a K row only meets a
+// score that is masked to -inf, and such a V row lies past the positions the
+// P.V loop visits, or is replaced by the new row.
 __device__ __forceinline__ void attn_prefetch(const AttnArgs& a, int s, int j, int T, int rrow, AttnPre& pf) {
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int g16 = lane & 15, pg = lane >> 4;
+  const int lane = threadIdx.x & 63, g16 = lane & 15, pg = lane >> 4;
   const int t0 = s * kAttnSplit;
+  constexpr int kBig = 0x7ffffff0;
+  const __amdgpu_buffer_rsrc_t rk = rsrc_n(a.kc, T > 0 ? kBig : 0);
+  const __amdgpu_buffer_rsrc_t rv = rsrc_n(a.vc, T > 0 ? kBig : 0);
+  const int last = T > 0 ? T - 1 : 0;
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
-    const int tp = t0 + 16 * wave + 4 * it + pg;
-    if (tp < T) {
-      ldc16(a.kc, tp * 512 + j * 256 + 16 * g16, pf.kreg[it]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) pf.kreg[it][e] = 0.0f;
-    }
+    const int tp = min(t0 + 4 * it + pg, last);
+    load16_rs(rk, (tp * 512 + j * 256 + 16 * g16) * 4, pf.k[it]);
   }
-  float* vl = attn_vlds();
-  const int nv = min(kAttnSplit, T - t0);   // rows before slot T (workgroup-uniform)
-  for (int i = wave; i < nv; i += 4)
-    __builtin_amdgcn_global_load_lds(static_cast<const void*>(a.vc + (size_t)(t0 + i) * 512 + j * 256 + 4 * lane),
-                                     (__attribute__((address_space(3))) void*)(vl + 256 * i), 16, 0, kSc1);
-  float* c = attn_clds();   // constants straight to LDS as well
-  typedef __attribute__((address_space(3))) void* lds_ptr;
-  if (wave == 0) __builtin_amdgcn_global_load_lds(static_cast<const void*>(a.qn + 4 * lane), (lds_ptr)c, 16, 0, 0);
-  if (wave == 1) __builtin_amdgcn_global_load_lds(static_cast<const void*>(a.kn + 4 * lane), (lds_ptr)(c + 256), 16, 0, 0);
-  if (wave == 2)
-    __builtin_amdgcn_global_load_lds(static_cast<const void*>(a.rope + (size_t)rrow * 64 + lane), (lds_ptr)(c + 512), 4, 0, 0);
+#pragma unroll
+  for (int u = 0; u < kAttnSplit; ++u) {
+    const int tp = min(t0 + u, last);
+    const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rv, (tp * 512 + j * 256 + 4 * lane) * 4, 0, 0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pf.v[u][e] = __uint_as_float(t[e]);
+  }
+  load16_rs(rsrc_n(a.qn, kBig), 64 * g16, pf.qn);
+  load16_rs(rsrc_n(a.kn, kBig), 64 * g16, pf.kn);
+  const __amdgpu_buffer_rsrc_t rr = rsrc_n(a.rope, kBig);
+  load16_rs(rr, (rrow * 64 + 16 * (g16 & 1)) * 4, pf.cs);
+  load16_rs(rr, (rrow * 64 + 32 + 16 * (g16 & 1)) * 4, pf.sn);
 }
 
 // nw16: this lane's 16 gains; cs16 / sn16: cos / sin[(16 g16 + e) & 31] (lanes g16 < 4 use them)
@@ -1278,108 +1328,86 @@ __device__ __forceinline__ void qk_norm_rope(float* x, const float* nw16, float 
 template <class IO>
 __device__ __forceinline__ bool attn_unit(const AttnArgs& a, int s, int j, int T, AttnPre& pf, IO& io) {
   const int Tn = T + 1;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int g16 = lane & 15, pg = lane >> 4;
-  __shared__ float sc[4][64];
-  __shared__ float pp[4][64];
-  const float* vl = attn_vlds();
+  const int lane = threadIdx.x & 63, g16 = lane & 15, pg = lane >> 4;
+  const int i = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = 4 * j + i;                  // query head of this wave
   const int t0 = s * kAttnSplit;
-  // qkv = q||gate (4096, interleaved per head) | k (512) | v (512)
   const bool owner = T / kAttnSplit == s;   // slot T lies in this split (attention.hpp:45-54)
-  float q[4][16];
-  float k[16];
-  float vT = 0.0f;
-  if (owner) {   // the four query heads, the new K row and V element in one poll
-    int idx[5];
+  const int tl = T - t0;                    // slot T within the split (owner)
+  // qkv = q||gate (4096, interleaved per head) | k (512) | v (512)
+  float q[16];
+  if (owner) {   // the query, the new K row and this lane's four new V elements in one poll
+    const int idx[2] = {h * 512 + 16 * g16, 4096 + j * 256 + 16 * g16};   // (attention.hpp:40)
+    const int iv[4] = {4608 + j * 256 + 4 * lane, 4608 + j * 256 + 4 * lane + 1, 4608 + j * 256 + 4 * lane + 2,
+                       4608 + j * 256 + 4 * lane + 3};
+    float t2[2][16], vT[4];
+    if (!io.template ld16vn<2, 4>(a.qkv, a.qkv_st, idx, t2, iv, vT)) return false;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) idx[i] = (4 * j + i) * 512 + 16 * g16;   // query half of head 4j+i (attention.hpp:40)
-    idx[4] = 4096 + j * 256 + 16 * g16;
-    float t5[5][16];
-    if (!io.template ld16v<5>(a.qkv, a.qkv_st, idx, t5, 4608 + j * 256 + t, vT)) return false;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) q[i][e] = t5[i][e];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) k[e] = t5[4][e];
-  } else {
-    int idx[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) idx[i] = (4 * j + i) * 512 + 16 * g16;
-    if (!io.template ld16<4>(a.qkv, a.qkv_st, idx, q)) return false;
-  }
-  io.mark(1);   // trace: q (and the new k, v) received
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // constants and V rows of this wave are in LDS
-  __syncthreads();
-  const float* cl = attn_clds();
-  {
-    float nw[16], cs[16], sn[16];
-    load16f(cl + 16 * g16, nw);
-    load16f(cl + 512 + 16 * (g16 & 1), cs);   // rope.hpp:30-41 uses cos/sin[(16 g16 + e) & 31]
-    load16f(cl + 544 + 16 * (g16 & 1), sn);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) qk_norm_rope(q[i], nw, a.eps, g16, cs, sn);
-    if (owner) {
-      load16f(cl + 256 + 16 * g16, nw);
-      qk_norm_rope(k, nw, a.eps, g16, cs, sn);
+    for (int e = 0; e < 16; ++e) q[e] = t2[0][e];
+    qk_norm_rope(t2[1], pf.kn, a.eps, g16, pf.cs, pf.sn);
+    if (i == 0) {   // wave 0 writes the new cache rows
+      if (pg == 0) stc16(a.kc, T * 512 + j * 256 + 16 * g16, t2[1]);
+      stc4(a.vc, T * 512 + j * 256 + 4 * lane, vT);
     }
-  }
-  if (owner) {
-    if (wave == 0 && pg == 0) stc16(a.kc, T * 512 + j * 256 + 16 * g16, k);
-    stcb(a.vc, T * 512 + j * 256 + t, vT);
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
-      const bool sel = t0 + 16 * wave + 4 * it + pg == T;
+      const bool sel = 4 * it + pg == tl;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) pf.kreg[it][e] = sel ? k[e] : pf.kreg[it][e];
+      for (int e = 0; e < 16; ++e) pf.k[it][e] = sel ? t2[1][e] : pf.k[it][e];
     }
+#pragma unroll
+    for (int u = 0; u < kAttnSplit; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pf.v[u][e] = u == tl ? vT[e] : pf.v[u][e];
+  } else {
+    const int idx[1] = {h * 512 + 16 * g16};
+    float t1[1][16];
+    if (!io.template ld16<1>(a.qkv, a.qkv_st, idx, t1)) return false;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) q[e] = t1[0][e];
   }
+  io.mark(1);   // trace: q (and the new k, v) received
+  qk_norm_rope(q, pf.qn, a.eps, g16, pf.cs, pf.sn);
+  // scores of positions t0 + 4 it + pg (the same value in the 16 lanes of group pg)
+  float sc[4], p[4];
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
-    const int tl = 16 * wave + 4 * it + pg;   // position within the split
-    const bool valid = t0 + tl < Tn;
+    float d = dot16_f32(q, pf.k[it], 0.0f);
+    d = xor_sum<16>(d);
+    sc[it] = t0 + 4 * it + pg < Tn ? d * 0.0625f : -__builtin_inff();
+  }
+  float m = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+  m = fmaxf(m, xor_perm<16>(m));
+  m = fmaxf(m, xor_perm<32>(m));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float d = dot16_f32(q[i], pf.kreg[it], 0.0f);
-      d = xor_sum<16>(d);
-      if (g16 == 0) sc[i][tl] = valid ? d * 0.0625f : -__builtin_inff();
-    }
+  for (int it = 0; it < 4; ++it) p[it] = t0 + 4 * it + pg < Tn ? dev_expf(sc[it] - m) : 0.0f;
+  // l: the 64-lane tree of p by position index (zeros past the split); pairs at
+  // distance 8 and 4 are the registers it, it + 2 and it, it + 1 of one lane,
+  // at distance 2 and 1 the lane groups pg ^ 2 (lane ^ 32) and pg ^ 1 (lane ^ 16)
+  float l = (p[0] + p[2]) + (p[1] + p[3]);
+  l = l + xor_perm<32>(l);
+  l = l + xor_perm<16>(l);
+  if (lane == 0) {
+    io.st1(a.pm, a.part_st, h * a.nsplit_max + s, m);
+    io.st1(a.pl, a.part_st, h * a.nsplit_max + s, l);
   }
-  __syncthreads();
-  {
-    const int i = wave;
-    const bool valid = t0 + lane < Tn;
-    const float sv = sc[i][lane];
-    const float m = xor_max<64>(valid ? sv : -__builtin_inff());
-    const float p = valid ? dev_expf(sv - m) : 0.0f;
-    const float l = xor_sum<64>(p);
-    pp[i][lane] = p;
-    if (lane == 0) {
-      io.st1(a.pm, a.part_st, (4 * j + i) * a.nsplit_max + s, m);
-      io.st1(a.pl, a.part_st, (4 * j + i) * a.nsplit_max + s, l);
-    }
-  }
-  __syncthreads();
   io.mark(2);   // trace: softmax of the split done
-  {   // thread t = dimension; position order (attention.hpp:80-86)
-    const int cnt = min(kAttnSplit, Tn - t0);
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  // P.V in position order (attention.hpp:80-86); p of position u sits in lane 16 (u & 3), register u >> 2
+  const int cnt = __builtin_amdgcn_readfirstlane(min(kAttnSplit, Tn - t0));
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int u = 0; u < kAttnSplit; ++u) {
-      if (u < cnt) {
-        const float v = (t0 + u == T) ? vT : vl[256 * u + t];
+  for (int u = 0; u < kAttnSplit; ++u) {
+    if (u < cnt) {
+      const float pu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[u >> 2]), 16 * (u & 3)));
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(pp[i][u], v, acc[i]);
-      }
+      for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(pu, pf.v[u][e], acc[e]);
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) io.st1(a.pacc, a.part_st, ((4 * j + i) * a.nsplit_max + s) * 256 + t, acc[i]);
   }
-  __syncthreads();
+  io.st4(a.pacc, a.part_st, (h * a.nsplit_max + s) * 256 + 4 * lane, acc);
   return true;
 }
 
-// Units u = blk, blk + nblk, ... of the 2 * ceil((T+1)/64) splits; T is the slot
+// Units u = blk, blk + nblk, ... of the 2 * ceil((T+1)/16) splits; T is the slot
 // of this token (past tokens = T).
 template <class IO>
 __device__ __forceinline__ bool attn_body(const AttnArgs& a, int T, int blk, int nblk, IO& io) {
@@ -1400,52 +1428,62 @@ __device__ __forceinline__ bool attn_body(const AttnArgs& a, int T, int blk, int
 }
 
 // Merge the splits of head h in split order; output gate (attention.hpp:89-92).
-constexpr int kCombineChunk = 8;
+// The split maxima and sums are read one split per thread; the partial sums of
+// this thread's dimension in batches of kCombineChunk splits.
+constexpr int kCombineChunk = 16;
 template <class IO>
 __device__ __forceinline__ bool combine_body(const AttnArgs& a, int T, int blk, IO& io) {
+  __shared__ float c_e[256], c_l[256], c_m[4];
   io.arrive();
   io.mark(0);   // trace: stage entry
   if (!io.wait()) return false;
-  const int h = blk, d = threadIdx.x;
+  const int h = blk, d = threadIdx.x, lane = d & 63, wave = d >> 6;
   if (h >= 8 || T < 0 || T >= a.max_ctx) return true;
+  const Raw graw = io.issue1(a.qkv, h * 512 + 256 + d);   // the output gate of dimension d
   const int Tn = T + 1;
   const int ns = (Tn + kAttnSplit - 1) / kAttnSplit;
   const int base = h * a.nsplit_max;
   float M = -__builtin_inff();
-  for (int s0 = 0; s0 < ns; s0 += kCombineChunk) {
-    int idx[kCombineChunk];
-    float m[kCombineChunk];
-#pragma unroll
-    for (int c = 0; c < kCombineChunk; ++c) idx[c] = base + min(s0 + c, ns - 1);
-    if (!io.template ldn<kCombineChunk>(a.pm, a.part_st, idx, m)) return false;
-#pragma unroll
-    for (int c = 0; c < kCombineChunk; ++c) M = fmaxf(M, m[c]);
+  for (int s0 = 0; s0 < ns; s0 += 256) {
+    float mv;
+    if (!io.ld1(a.pm, a.part_st, base + min(s0 + d, ns - 1), mv)) return false;
+    M = fmaxf(M, mv);
   }
+  M = xor_max<64>(M);
+  if (lane == 0) c_m[wave] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(c_m[0], c_m[1]), fmaxf(c_m[2], c_m[3]));
   float L = 0.0f, ctx = 0.0f;
-  for (int s0 = 0; s0 < ns; s0 += kCombineChunk) {
-    int idx[kCombineChunk], ia[kCombineChunk];
-    float m[kCombineChunk], l[kCombineChunk], pa[kCombineChunk];
-#pragma unroll
-    for (int c = 0; c < kCombineChunk; ++c) {
-      idx[c] = base + min(s0 + c, ns - 1);
-      ia[c] = idx[c] * 256 + d;
+  for (int s0 = 0; s0 < ns; s0 += 256) {
+    const int n = min(256, ns - s0);
+    if (d < n) {
+      float mv, lv;
+      if (!io.ld1(a.pm, a.part_st, base + s0 + d, mv) || !io.ld1(a.pl, a.part_st, base + s0 + d, lv)) return false;
+      c_e[d] = dev_expf(mv - M);
+      c_l[d] = lv;
     }
-    if (!io.template ldn<kCombineChunk>(a.pm, a.part_st, idx, m)) return false;
-    if (!io.template ldn<kCombineChunk>(a.pl, a.part_st, idx, l)) return false;
-    if (!io.template ldn<kCombineChunk>(a.pacc, a.part_st, ia, pa)) return false;
+    __syncthreads();
+    for (int c0 = 0; c0 < n; c0 += kCombineChunk) {
+      int ia[kCombineChunk];
+      float pa[kCombineChunk];
 #pragma unroll
-    for (int c = 0; c < kCombineChunk; ++c) {
-      if (s0 + c < ns) {
-        const float e = dev_expf(m[c] - M);
-        L = L + l[c] * e;
-        ctx = ctx + pa[c] * e;
+      for (int c = 0; c < kCombineChunk; ++c) ia[c] = (base + s0 + min(c0 + c, n - 1)) * 256 + d;
+      if (!io.template ldn<kCombineChunk>(a.pacc, a.part_st, ia, pa)) return false;
+#pragma unroll
+      for (int c = 0; c < kCombineChunk; ++c) {
+        if (c0 + c < n) {
+          const float e = c_e[c0 + c];
+          L = L + c_l[c0 + c] * e;
+          ctx = ctx + pa[c] * e;
+        }
       }
     }
+    __syncthreads();
   }
   io.mark(1);   // trace: all split partials received
   const float invL = 1.0f / L;
   float gate;
-  if (!io.ld1(a.qkv, a.qkv_st, h * 512 + 256 + d, gate)) return false;
+  if (!io.resolve1(graw, a.qkv, a.qkv_st, h * 512 + 256 + d, gate)) return false;
   io.st1(a.og, a.og_st, h * 256 + d, (ctx * invL) * dev_sigmoid(gate));
   return true;
 }
