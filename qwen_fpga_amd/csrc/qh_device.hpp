@@ -260,19 +260,38 @@ __device__ __forceinline__ void* wave_uniform(const void* p) {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t coh_rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(wave_uniform(base), (short)0, 0x7ffffff0, 0x00020000);
 }
+// Global / LDS views of generic pointers.  An access through a generic
+// pointer is a flat_* instruction, which the hardware counts against both the
+// vector-memory and the LDS counters: every wait for an LDS read would then
+// also wait for the flat accesses in flight (weight prefetches, state
+// stores).  Through these views the compiler emits global_* (vector-memory
+// counter only) or ds_* instructions.  The pointer must address that memory.
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* as_global(const T* p) {
+  return (const __attribute__((address_space(1))) T*)p;
+}
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* as_global_w(T* p) {
+  return (__attribute__((address_space(1))) T*)p;
+}
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(3))) T* as_lds(const T* p) {
+  return (const __attribute__((address_space(3))) T*)p;
+}
+
 __device__ __forceinline__ float ldc(const float* p) {
   return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_AGENT));
 }
 __device__ __forceinline__ int ldc_i(const int* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load(as_global(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void stc(float* p, float v) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void stc_i(int* p, int v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(as_global_w(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // base[idx] (uniform base, per-lane idx)
 __device__ __forceinline__ float ldcb(const float* base, int idx) {

@@ -202,6 +202,7 @@ void build_layers(const qh_engine* e, int l0, int l1, bool embed, Bufs& B, std::
       d.S = e->rec + (size_t)li * kLH * kLK * kLV;
       d.o = B.take(kLH * kLV, e->o);
       d.o_st = sB;
+      if (tag) d.gt = B.take(2 * kLH, e->gb);
       d.done = done;
       Stage sd;
       sd.kind = ST_DELTANET;

@@ -142,6 +142,8 @@ struct DnArgs {
   int mode = M_W8A16;
   float* S = nullptr;            // [16][128][128]
   float* o = nullptr;            // [16][128]
+  float* gt = nullptr;           // tagged g[16] beta[16]: the gates, computed by workgroups of this
+                                 // stage that own no head quarter (persistent kernel; null: each unit)
   int normalize = 1;             // l2norm q,k and scale q (0: given already normalized)
   int heads = 16;                // heads to process (1 for the single-head op)
   const int* done = nullptr;

@@ -136,6 +136,28 @@ struct PlainIO {
     v1 = o1[0];
     return ok;
   }
+  // ld16vn in two steps, so that loads issued in between queue behind it.
+  template <int N, int M>
+  struct Poll16 {
+    float v[N][16];
+    float v1[M];
+  };
+  template <int N, int M>
+  __device__ __forceinline__ void poll_issue(const float* base, const int (&idx)[N], const int (&idx1)[M],
+                                             Poll16<N, M>& P) {
+    ld16vn<N, M>(base, 0, idx, P.v, idx1, P.v1);
+  }
+  template <int N, int M>
+  __device__ __forceinline__ bool poll_finish(const float*, int, const int (&)[N], const int (&)[M], Poll16<N, M>& P,
+                                              float (&v)[N][16], float (&v1)[M]) {
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) v[j][e] = P.v[j][e];
+#pragma unroll
+    for (int m = 0; m < M; ++m) v1[m] = P.v1[m];
+    return true;
+  }
   // A vector the workgroup copied to LDS earlier in this stage program (none here).
   __device__ __forceinline__ const float* cached(const float*, int) const { return nullptr; }
   // Workgroup copy of a vector, in two steps around the stage's weight loads:
@@ -324,42 +346,58 @@ struct TagIO {
   __device__ __forceinline__ void st1i(int* base, int st, int idx, int v) {
     st1(reinterpret_cast<float*>(base), st, idx, __int_as_float(v));
   }
+  // N 16-element chunks and M single elements of one vector, polled together.
+  // poll_issue makes the first attempt; loads issued after it return after it,
+  // so work placed between the two steps overlaps the hand-over wait.
   template <int N, int M>
-  __device__ __forceinline__ bool ld16vn(const float* base, int st, const int (&idx)[N], float (&v)[N][16],
-                                         const int (&idx1)[M], float (&v1)[M]) {
-    const uint32_t tg = tag(st);
-    const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
+  struct Poll16 {
     u32x4 u[N][8];
     u32x2 u1[M];
-    auto issue = [&]() {
-      issue16<N>(rs, idx, u);
+  };
+  template <int N, int M>
+  __device__ __forceinline__ void poll_issue(const float* base, const int (&idx)[N], const int (&idx1)[M],
+                                             Poll16<N, M>& P) {
+    const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
+    issue16<N>(rs, idx, P.u);
 #pragma unroll
-      for (int m = 0; m < M; ++m) u1[m] = __builtin_amdgcn_raw_buffer_load_b64(rs, idx1[m] * 8, 0, kSc1);
-    };
+    for (int m = 0; m < M; ++m) P.u1[m] = __builtin_amdgcn_raw_buffer_load_b64(rs, idx1[m] * 8, 0, kSc1);
+    asm volatile("" ::: "memory");   // nothing issued later may move ahead of these loads
+  }
+  template <int N, int M>
+  __device__ __forceinline__ bool poll_finish(const float* base, int st, const int (&idx)[N], const int (&idx1)[M],
+                                              Poll16<N, M>& P, float (&v)[N][16], float (&v1)[M]) {
+    const uint32_t tg = tag(st);
     auto tags = [&]() {
       bool ok = true;
 #pragma unroll
-      for (int m = 0; m < M; ++m) ok = ok & (u1[m][1] == tg);
-      return tags16<N>(u, tg) && wave_all(ok);
+      for (int m = 0; m < M; ++m) ok = ok & (P.u1[m][1] == tg);
+      return tags16<N>(P.u, tg) && wave_all(ok);
     };
-    issue();
     if (!tags()) {
+      const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
       unsigned polls = 0;
       do {
         if (!again(polls) || !sample(rs, idx1[M - 1], tg, polls)) return false;
-        issue();
+        poll_issue<N, M>(base, idx, idx1, P);
       } while (!tags());
     }
 #pragma unroll
     for (int j = 0; j < N; ++j)
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        v[j][2 * k] = __uint_as_float(u[j][k][0]);
-        v[j][2 * k + 1] = __uint_as_float(u[j][k][2]);
+        v[j][2 * k] = __uint_as_float(P.u[j][k][0]);
+        v[j][2 * k + 1] = __uint_as_float(P.u[j][k][2]);
       }
 #pragma unroll
-    for (int m = 0; m < M; ++m) v1[m] = __uint_as_float(u1[m][0]);
+    for (int m = 0; m < M; ++m) v1[m] = __uint_as_float(P.u1[m][0]);
     return true;
+  }
+  template <int N, int M>
+  __device__ __forceinline__ bool ld16vn(const float* base, int st, const int (&idx)[N], float (&v)[N][16],
+                                         const int (&idx1)[M], float (&v1)[M]) {
+    Poll16<N, M> P;
+    poll_issue<N, M>(base, idx, idx1, P);
+    return poll_finish<N, M>(base, st, idx, idx1, P, v, v1);
   }
   template <int N>
   __device__ __forceinline__ bool ld16v(const float* base, int st, const int (&idx)[N], float (&v)[N][16], int idx1,
@@ -556,36 +594,34 @@ __device__ __forceinline__ int row_of_lane(int lane) {
   return R == 1 ? 0 : (lane >> (R == 8 ? 3 : R == 4 ? 4 : 5)) & (R - 1);
 }
 
-__device__ __forceinline__ void load16f(const float* p, float* v) {
-  const float4* q = reinterpret_cast<const float4*>(p);
+// 16 floats from global memory (load16g) or LDS (load16l), 16-byte aligned
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void load16g(const float* p, float* v) {
+  const __attribute__((address_space(1))) f32x4* q = as_global(reinterpret_cast<const f32x4*>(p));
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const float4 t = q[k];
-    v[4 * k + 0] = t.x;
-    v[4 * k + 1] = t.y;
-    v[4 * k + 2] = t.z;
-    v[4 * k + 3] = t.w;
+    const f32x4 t = q[k];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[4 * k + e] = t[e];
   }
 }
-__device__ __forceinline__ void store16f(float* p, const float* v) {
-  float4* q = reinterpret_cast<float4*>(p);
+__device__ __forceinline__ void load16l(const float* p, float* v) {
+  const __attribute__((address_space(3))) f32x4* q = as_lds(reinterpret_cast<const f32x4*>(p));
 #pragma unroll
-  for (int k = 0; k < 4; ++k) q[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+  for (int k = 0; k < 4; ++k) {
+    const f32x4 t = q[k];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[4 * k + e] = t[e];
+  }
 }
+// 16 int8 from global memory
 __device__ __forceinline__ void load16b(const int8_t* p, uint32_t* w) {
-  const uint4 t = *reinterpret_cast<const uint4*>(p);
-  w[0] = t.x;
-  w[1] = t.y;
-  w[2] = t.z;
-  w[3] = t.w;
+  const u32x4 t = *as_global(reinterpret_cast<const u32x4*>(p));
+#pragma unroll
+  for (int e = 0; e < 4; ++e) w[e] = t[e];
 }
 __device__ __forceinline__ float i8_at(const uint32_t* w, int e) {
   return (float)(int)(int8_t)(w[e >> 2] >> (8 * (e & 3)));
-}
-
-__device__ __forceinline__ float seg_scale(const Seg& g, int row) {
-  if (g.kind == SEG_PAIR) return (row & 1) ? g.sw2[row >> 1] : g.sw[row >> 1];
-  return g.sw[row];
 }
 
 // Per-row epilogue inputs, loaded by every lane for its row at batch start.
@@ -652,7 +688,7 @@ __device__ __forceinline__ void gemv_epilogue(const Seg& g, int ost, int lane, i
       break;
     case E_ACC:
       io.st1(g.out, ost, myrow, y);
-      g.acc_out[myrow] = acci;
+      as_global_w(g.acc_out)[myrow] = acci;
       break;
     case E_GATE_B:
       io.st1(g.out, ost, myrow, dev_sigmoid(y));
@@ -666,7 +702,7 @@ __device__ __forceinline__ void gemv_epilogue(const Seg& g, int ost, int lane, i
       acc = acc + x.a2 * x.w1;
       acc = acc + x.a3 * x.w2;
       acc = acc + y * x.w3;
-      *reinterpret_cast<float4*>(g.c2 + (size_t)myrow * 4) = make_float4(x.a1, x.a2, x.a3, y);
+      *as_global_w(reinterpret_cast<f32x4*>(g.c2 + (size_t)myrow * 4)) = f32x4{x.a1, x.a2, x.a3, y};
       io.st1(g.out, ost, myrow, dev_silu(acc));
       break;
     }
@@ -746,7 +782,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int c = min(lane + 64 * j, nchunk - 1);
-      load16f(a.nw + (PRO == P_GATED ? ((16 * c) & 127) : 16 * c), nwv16[j]);
+      load16g(a.nw + (PRO == P_GATED ? ((16 * c) & 127) : 16 * c), nwv16[j]);
     }
   }
   if (!io.wait()) return false;
@@ -771,7 +807,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
   uint32_t xq[NCH][4];   // int8 activation (W8A8)
   float xs = 1.0f;       // activation scale (W8A8)
   if constexpr (PRO == P_LOADQ) {
-    xs = *a.sx;
+    xs = *as_global(a.sx);
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int c = lane + 64 * j;
@@ -784,7 +820,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
     if (PRO == P_NORM && a.emb != nullptr) {   // embed_row (gemv.hpp:76-84)
       const int tok = a.tok != nullptr ? ldc_i(a.tok) : tokv;
       const int8_t* er = a.emb + (size_t)tok * K;
-      const float es = a.emb_s[tok];
+      const float es = as_global(a.emb_s)[tok];
 #pragma unroll
       for (int j = 0; j < NCH; ++j) {
         const int c = lane + 64 * j;
@@ -802,7 +838,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
     } else {
 #pragma unroll
       for (int j = 0; j < NCH; ++j) {
-        load16f(xl + 16 * min(lane + 64 * j, nchunk - 1), xv[j]);
+        load16l(xl + 16 * min(lane + 64 * j, nchunk - 1), xv[j]);
         if (lane + 64 * j >= nchunk)
 #pragma unroll
           for (int e = 0; e < 16; ++e) xv[j][e] = 0.0f;
@@ -823,7 +859,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
     } else if constexpr (PRO == P_GATED) {   // heads of 128 = groups of 8 lanes; z holds silu(z)
       float zs[NCH][16];
 #pragma unroll
-      for (int j = 0; j < NCH; ++j) load16f(zl + 16 * (lane + 64 * j), zs[j]);
+      for (int j = 0; j < NCH; ++j) load16l(zl + 16 * (lane + 64 * j), zs[j]);
 #pragma unroll
       for (int j = 0; j < NCH; ++j) {
         float ss = dot16_f32(xv[j], xv[j], 0.0f);
@@ -878,7 +914,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
           for (int r = 0; r < R; ++r) {
             if (row0 + r < g.rows) {
               float wf[16];
-              load16f(g.wf + (size_t)(row0 + r) * K + 16 * c, wf);
+              load16g(g.wf + (size_t)(row0 + r) * K + 16 * c, wf);
               pf[r] = dot16_f32(wf, xv[j], pf[r]);
             }
           }
@@ -987,12 +1023,12 @@ __device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, 
   head_load(a, b, total, lane, rl, w0, sc0);   // two batches in flight before the norm prologue
   head_load(a, b + stride, total, lane, rl, w1, sc1);
   float xv[16], nw[16];
-  load16f(a.nw + 16 * lane, nw);
+  load16g(a.nw + 16 * lane, nw);
   if (!io.wait()) return false;
   {
     float* hl = io.slot();
     if (!io.stage_finish(a.h, a.h_st, 1024, hl, vh)) return false;
-    load16f(hl + 16 * lane, xv);
+    load16l(hl + 16 * lane, xv);
   }
   float ss = dot16_f32(xv, xv, 0.0f);
   ss = xor_sum<64>(ss);
@@ -1052,16 +1088,20 @@ __device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, 
 // ===========================================================================
 // Gated DeltaNet recurrent step (deltanet.hpp:58-127 and the l2norm / q-scale
 // of deltanet.hpp:166-169).  Unit (head h, quarter vq) owns S[h][:, 32 vq ..
-// 32 vq + 31]: thread (kg, vl) holds the 16 rows k = 16 kg .. 16 kg + 15 of
-// column v = 32 vq + vl.  Sweep A decays S and forms the k-group partial of
-// k^T S; the 8 group partials meet in LDS and are added by the pairwise tree
-// (offsets 4, 2, 1); delta = (v - kv) * beta; sweep B applies the rank-1
-// update and forms q^T S_new the same way.  S is read and written once per
-// step, always by the same unit.
+// 32 vq + 31]; wave w takes columns v = 32 vq + 8 w + (lane >> 3) and lane
+// group kg = lane & 7 the 16 rows k = 16 kg .. 16 kg + 15 of its column, so
+// the eight k-groups of a column sit in one lane octet and meet by the xor
+// tree of offsets 4, 2, 1 (the pairwise tree of the device order).  Each lane
+// holds the q and k chunks of its k-group and normalises them itself (the
+// octet holds whole vectors).  Sweep A decays S and forms the k-group partial
+// of k^T S; delta = (v - kv) * beta; sweep B applies the rank-1 update and
+// forms q^T S_new.  No workgroup barrier, no LDS.  S is read and written once
+// per step, always by the same unit.
 // ===========================================================================
-// Head h's gate projections from the layer input (see DnArgs), on one wave;
-// lane 0 returns (g, beta).  Same operations as the in_proj prologue and its
-// fp32 segments, so the values are bit-identical to computing them there.
+// Head h's gate projections from the layer input (see DnArgs), computed by a
+// whole wave; every lane returns (g, beta).  Same operations as the in_proj
+// prologue and its fp32 segments, so the values are bit-identical to
+// computing them there.
 template <class IO>
 __device__ __forceinline__ bool deltanet_gates(const DnArgs& a, int h, int tokv, float& g, float& beta, IO& io) {
   const int lane = threadIdx.x & 63;
@@ -1070,11 +1110,11 @@ __device__ __forceinline__ bool deltanet_gates(const DnArgs& a, int h, int tokv,
     const int tok = a.tok != nullptr ? ldc_i(a.tok) : tokv;
     uint32_t t4[4];
     load16b(a.emb + (size_t)tok * 1024 + 16 * lane, t4);
-    const float es = a.emb_s[tok];
+    const float es = as_global(a.emb_s)[tok];
 #pragma unroll
     for (int e = 0; e < 16; ++e) xv[e] = i8_at(t4, e) * es;
   } else if (const float* xl = io.cached(a.gx, a.gx_st)) {   // the in_proj stage's copy
-    load16f(xl + 16 * lane, xv);
+    load16l(xl + 16 * lane, xv);
   } else {
     int idx[1] = {16 * lane};
     float t1[1][16];
@@ -1084,7 +1124,7 @@ __device__ __forceinline__ bool deltanet_gates(const DnArgs& a, int h, int tokv,
   }
   if (a.gx_norm != nullptr) {   // norm.hpp:13-20
     float nw[16];
-    load16f(a.gx_norm + 16 * lane, nw);
+    load16g(a.gx_norm + 16 * lane, nw);
     float ss = dot16_f32(xv, xv, 0.0f);
     ss = xor_sum<64>(ss);
     const float inv = 1.0f / sqrtf(ss / 1024.0f + a.eps);
@@ -1102,139 +1142,116 @@ __device__ __forceinline__ bool deltanet_gates(const DnArgs& a, int h, int tokv,
     for (int e = 0; e < 16; ++e) xv[e] = (float)quant_one_r(xv[e], xs, rs) * xs;
   }
   float w[16];
-  load16f(a.wb + (size_t)h * 1024 + 16 * lane, w);
+  load16g(a.wb + (size_t)h * 1024 + 16 * lane, w);
   const float yb = xor_sum<64>(dot16_f32(w, xv, 0.0f));
-  load16f(a.wa + (size_t)h * 1024 + 16 * lane, w);
+  load16g(a.wa + (size_t)h * 1024 + 16 * lane, w);
   const float ya = xor_sum<64>(dot16_f32(w, xv, 0.0f));
   beta = dev_sigmoid(yb);
-  g = -dev_expf(a.A_log[h]) * dev_softplus(ya + a.dt_bias[h]);
+  g = -dev_expf(as_global(a.A_log)[h]) * dev_softplus(ya + as_global(a.dt_bias)[h]);
   return true;
 }
 
+// gates_given: g and beta come from the tagged vector a.gt (written by the
+// gate workgroups of this stage) instead of being computed by every wave.
 template <class IO>
-__device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool valid, IO& io, int tokv) {
+__device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool valid, bool gates_given, IO& io,
+                                              int tokv) {
   const int h = unit / kDnVQuarters, vq = unit % kDnVQuarters;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int vl = t & 31, kg = t >> 5, v = vq * 32 + vl;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kg = lane & 7, v = vq * 32 + 8 * wave + (lane >> 3);
   float* Sh = a.S + (size_t)h * 128 * 128;
-  __shared__ float gbs[2];
   io.arrive();
   io.mark(0);   // trace: stage entry
+  // convd = q (2048) | k (2048) | v (2048), post-conv; chunks of this lane's k-group
+  const int idx[2] = {h * 128 + 16 * kg, 2048 + h * 128 + 16 * kg};
+  const int iv[1] = {4096 + h * 128 + v};
+  typename IO::template Poll16<2, 1> P;
   float s[16];
-  bool ok = true;
+  float g = 0.0f, beta = 0.0f;
+  Raw rg, rb;
   if (valid) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = Sh[(kg * 16 + i) * 128 + v];   // state tile in flight first
-    if (a.wa != nullptr && wave == 0) {   // inputs final before in_proj: off the critical path
-      float g0 = 0.0f, b0 = 0.0f;
-      ok = deltanet_gates(a, h, tokv, g0, b0, io);
-      if (lane == 0) {
-        gbs[0] = g0;
-        gbs[1] = b0;
-      }
+    io.template poll_issue<2, 1>(a.convd, idx, iv, P);
+    if (gates_given) {
+      rg = io.issue1(a.gt, h);
+      rb = io.issue1(a.gt, 16 + h);
     }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = as_global(Sh)[(kg * 16 + i) * 128 + v];
+    // inputs final before in_proj: computed while the hand-over is in flight
+    if (!gates_given && a.wa != nullptr && !deltanet_gates(a, h, tokv, g, beta, io)) return false;
   }
-  if (!ok) return false;
   if (!io.wait()) return false;
   if (!valid) return true;
-  __shared__ float qs[128], ks[128];
-  __shared__ float part[8][32];
-  __shared__ float dl[32];
-  float g = 0.0f, beta = 0.0f;
   if constexpr (!IO::kTagged) {   // gates given by the op-level caller
     if (a.wa == nullptr) {
       g = ldcb(a.gb, h);
       beta = ldcb(a.gb, 16 + h);
     }
   }
-  float vv;
-  float qk[16];   // wave 0: q, wave 1: k (waves 2, 3 read q too and drop it); lanes 0..7 hold 16 each
-  {
-    int idx[1] = {((wave & 1) ? 2048 : 0) + h * 128 + 16 * min(lane, 7)};
-    float t1[1][16];
-    if (!io.template ld16v<1>(a.convd, a.convd_st, idx, t1, 4096 + h * 128 + v, vv)) return false;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) qk[e] = t1[0][e];
-  }
+  float qk[2][16], vv[1];
+  if (!io.template poll_finish<2, 1>(a.convd, a.convd_st, idx, iv, P, qk, vv)) return false;
+  if (gates_given && (!io.resolve1(rg, a.gt, a.o_st, h, g) || !io.resolve1(rb, a.gt, a.o_st, 16 + h, beta)))
+    return false;
   io.mark(1);   // trace: q, k, v of the head received
-  if (wave < 2) {
-    float x[16];
-    float ss = 0.0f;
+  if (a.normalize) {   // l2norm (deltanet.hpp:134); q also scaled by 1/sqrt(128) (deltanet.hpp:168-169)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) x[e] = lane < 8 ? qk[e] : 0.0f;
-    if (lane < 8) ss = dot16_f32(x, x, 0.0f);
-    if (a.normalize) {
+    for (int w = 0; w < 2; ++w) {
+      float ss = dot16_f32(qk[w], qk[w], 0.0f);
       ss = xor_sum<8>(ss);
-      const float inv = 1.0f / sqrtf(ss + 1e-6f);   // deltanet.hpp:134
+      const float inv = 1.0f / sqrtf(ss + 1e-6f);
 #pragma unroll
-      for (int e = 0; e < 16; ++e) x[e] = x[e] * inv;
-      if (wave == 0) {
-        const float sc = 1.0f / sqrtf(128.0f);   // deltanet.hpp:168-169
-#pragma unroll
-        for (int e = 0; e < 16; ++e) x[e] = x[e] * sc;
-      }
+      for (int e = 0; e < 16; ++e) qk[w][e] = qk[w][e] * inv;
     }
-    if (lane < 8) store16f((wave == 0 ? qs : ks) + 16 * lane, x);
-  }
-  __syncthreads();
-  if (a.wa != nullptr) {
-    g = gbs[0];
-    beta = gbs[1];
+    const float sc = 1.0f / sqrtf(128.0f);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) qk[0][e] = qk[0][e] * sc;
   }
   const float gexp = dev_expf(g);
   float p = 0.0f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {   // sweep A
-    const int k = kg * 16 + i;
     s[i] = s[i] * gexp;
-    p = p + s[i] * ks[k];
+    p = p + s[i] * qk[1][i];
   }
-  part[kg][vl] = p;
-  __syncthreads();
-  if (kg == 0) {
-    float pp[8];
-#pragma unroll
-    for (int gi = 0; gi < 8; ++gi) pp[gi] = part[gi][vl];
-#pragma unroll
-    for (int off = 4; off >= 1; off >>= 1)
-#pragma unroll
-      for (int gi = 0; gi < off; ++gi) pp[gi] = pp[gi] + pp[gi + off];
-    dl[vl] = (vv - pp[0]) * beta;
-  }
-  __syncthreads();
+  p = xor_sum<8>(p);
+  const float d = (vv[0] - p) * beta;
   io.mark(2);   // trace: delta computed (sweep A done)
-  const float d = dl[vl];
   p = 0.0f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {   // sweep B: reads the updated S
-    const int k = kg * 16 + i;
-    s[i] = s[i] + ks[k] * d;
-    p = p + s[i] * qs[k];
-    Sh[k * 128 + v] = s[i];
+    s[i] = s[i] + qk[1][i] * d;
+    p = p + s[i] * qk[0][i];
+    as_global_w(Sh)[(kg * 16 + i) * 128 + v] = s[i];
   }
-  part[kg][vl] = p;
-  __syncthreads();
-  if (kg == 0) {
-    float pp[8];
-#pragma unroll
-    for (int gi = 0; gi < 8; ++gi) pp[gi] = part[gi][vl];
-#pragma unroll
-    for (int off = 4; off >= 1; off >>= 1)
-#pragma unroll
-      for (int gi = 0; gi < off; ++gi) pp[gi] = pp[gi] + pp[gi + off];
-    io.st1(a.o, a.o_st, h * 128 + v, pp[0]);
-  }
-  __syncthreads();
+  p = xor_sum<8>(p);
+  if (kg == 0) io.st1(a.o, a.o_st, h * 128 + v, p);
   return true;
 }
 
 // All heads * kDnVQuarters units; the first one of each workgroup prefetches.
+// With tagged I/O and enough workgroups, workgroups units .. units + heads - 1
+// compute the gates of one head each (wave 0) and hand them over.
 template <class IO>
 __device__ __forceinline__ bool deltanet_all(const DnArgs& a, int blk, int nblk, IO& io, int tokv) {
   const int units = a.heads * kDnVQuarters;
-  if (!deltanet_body(a, blk, blk < units, io, tokv)) return false;
+  const bool gate_wgs = IO::kTagged && a.gt != nullptr && a.wa != nullptr && nblk >= units + a.heads;
+  if (gate_wgs && blk >= units) {
+    io.arrive();
+    io.mark(0);   // trace: stage entry
+    const int h = blk - units;
+    if (h < a.heads && threadIdx.x < 64) {
+      float g = 0.0f, beta = 0.0f;
+      if (!deltanet_gates(a, h, tokv, g, beta, io)) return false;
+      if (threadIdx.x == 0) {
+        io.st1(a.gt, a.o_st, h, g);
+        io.st1(a.gt, a.o_st, 16 + h, beta);
+      }
+    }
+    return true;
+  }
+  if (!deltanet_body(a, blk, blk < units, gate_wgs, io, tokv)) return false;
   for (int u = blk + nblk; u < units; u += nblk)
-    if (!deltanet_body(a, u, true, io, tokv)) return false;
+    if (!deltanet_body(a, u, true, gate_wgs, io, tokv)) return false;
   return true;
 }
 
@@ -1325,25 +1342,39 @@ __device__ __forceinline__ void qk_norm_rope(float* x, const float* nw16, float 
   }
 }
 
-template <class IO>
-__device__ __forceinline__ bool attn_unit(const AttnArgs& a, int s, int j, int T, AttnPre& pf, IO& io) {
+// OWNER: slot T lies in this split (attention.hpp:45-54).  The poll of the
+// unit's inputs is issued first and the prefetch after it, so the poll does
+// not queue behind the cache rows.
+template <bool OWNER, class IO>
+__device__ __forceinline__ bool attn_unit(const AttnArgs& a, int s, int j, int T, int rrow, IO& io) {
   const int Tn = T + 1;
   const int lane = threadIdx.x & 63, g16 = lane & 15, pg = lane >> 4;
   const int i = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = 4 * j + i;                  // query head of this wave
   const int t0 = s * kAttnSplit;
-  const bool owner = T / kAttnSplit == s;   // slot T lies in this split (attention.hpp:45-54)
-  const int tl = T - t0;                    // slot T within the split (owner)
-  // qkv = q||gate (4096, interleaved per head) | k (512) | v (512)
-  float q[16];
-  if (owner) {   // the query, the new K row and this lane's four new V elements in one poll
-    const int idx[2] = {h * 512 + 16 * g16, 4096 + j * 256 + 16 * g16};   // (attention.hpp:40)
-    const int iv[4] = {4608 + j * 256 + 4 * lane, 4608 + j * 256 + 4 * lane + 1, 4608 + j * 256 + 4 * lane + 2,
-                       4608 + j * 256 + 4 * lane + 3};
-    float t2[2][16], vT[4];
-    if (!io.template ld16vn<2, 4>(a.qkv, a.qkv_st, idx, t2, iv, vT)) return false;
+  const int tl = T - t0;                    // slot T within the split (OWNER)
+  // qkv = q||gate (4096, interleaved per head) | k (512) | v (512): the query
+  // (attention.hpp:40); the owner also takes the new K row and this lane's
+  // four new V elements
+  constexpr int NQ = OWNER ? 2 : 1, NV = OWNER ? 4 : 1;
+  int idx[NQ], iv[NV];
+  idx[0] = h * 512 + 16 * g16;
+  if constexpr (OWNER) {
+    idx[1] = 4096 + j * 256 + 16 * g16;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) q[e] = t2[0][e];
+    for (int e = 0; e < 4; ++e) iv[e] = 4608 + j * 256 + 4 * lane + e;
+  } else {
+    iv[0] = idx[0];   // (an element of the query chunk)
+  }
+  typename IO::template Poll16<NQ, NV> P;
+  io.template poll_issue<NQ, NV>(a.qkv, idx, iv, P);
+  AttnPre pf;
+  attn_prefetch(a, s, j, T, rrow, pf);
+  if (!io.wait()) return false;
+  float t2[NQ][16], vT[NV];
+  if (!io.template poll_finish<NQ, NV>(a.qkv, a.qkv_st, idx, iv, P, t2, vT)) return false;
+  io.mark(1);   // trace: q (and the new k, v) received
+  if constexpr (OWNER) {
     qk_norm_rope(t2[1], pf.kn, a.eps, g16, pf.cs, pf.sn);
     if (i == 0) {   // wave 0 writes the new cache rows
       if (pg == 0) stc16(a.kc, T * 512 + j * 256 + 16 * g16, t2[1]);
@@ -1359,14 +1390,8 @@ __device__ __forceinline__ bool attn_unit(const AttnArgs& a, int s, int j, int T
     for (int u = 0; u < kAttnSplit; ++u)
 #pragma unroll
       for (int e = 0; e < 4; ++e) pf.v[u][e] = u == tl ? vT[e] : pf.v[u][e];
-  } else {
-    const int idx[1] = {h * 512 + 16 * g16};
-    float t1[1][16];
-    if (!io.template ld16<1>(a.qkv, a.qkv_st, idx, t1)) return false;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) q[e] = t1[0][e];
   }
-  io.mark(1);   // trace: q (and the new k, v) received
+  float* q = t2[0];
   qk_norm_rope(q, pf.qn, a.eps, g16, pf.cs, pf.sn);
   // scores of positions t0 + 4 it + pg (the same value in the 16 lanes of group pg)
   float sc[4], p[4];
@@ -1417,12 +1442,11 @@ __device__ __forceinline__ bool attn_body(const AttnArgs& a, int T, int blk, int
   if (blk >= units) return true;
   io.mark(0);   // trace: stage entry
   const int rrow = a.rope_row != nullptr ? ldc_i(a.rope_row) : T;
-  AttnPre pf;
-  attn_prefetch(a, blk >> 1, blk & 1, T, rrow, pf);
-  if (!io.wait()) return false;
   for (int u = blk; u < units; u += nblk) {
-    if (u != blk) attn_prefetch(a, u >> 1, u & 1, T, rrow, pf);
-    if (!attn_unit(a, u >> 1, u & 1, T, pf, io)) return false;
+    const int s = u >> 1, j = u & 1;
+    const bool done = T / kAttnSplit == s ? attn_unit<true>(a, s, j, T, rrow, io)
+                                          : attn_unit<false>(a, s, j, T, rrow, io);
+    if (!done) return false;
   }
   return true;
 }
