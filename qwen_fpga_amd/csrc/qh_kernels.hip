@@ -169,7 +169,7 @@ hipError_t launch_attn(const AttnArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 hipError_t launch_attn_combine(const AttnArgs& a, hipStream_t s) {
-  attn_combine_kernel<<<8, 256, 0, s>>>(a);
+  attn_combine_kernel<<<kCombineWGs, 256, 0, s>>>(a);
   return hipGetLastError();
 }
 

@@ -373,13 +373,16 @@ struct TagIO {
       for (int m = 0; m < M; ++m) ok = ok & (P.u1[m][1] == tg);
       return tags16<N>(P.u, tg) && wave_all(ok);
     };
-    if (!tags()) {
+    const bool hit = tags();
+    mark(3);   // trace: first poll returned
+    if (!hit) {
       const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
       unsigned polls = 0;
       do {
         if (!again(polls) || !sample(rs, idx1[M - 1], tg, polls)) return false;
         poll_issue<N, M>(base, idx, idx1, P);
       } while (!tags());
+      mark(4);   // trace: complete after a repoll
     }
 #pragma unroll
     for (int j = 0; j < N; ++j)
@@ -1452,59 +1455,65 @@ __device__ __forceinline__ bool attn_body(const AttnArgs& a, int T, int blk, int
 }
 
 // Merge the splits of head h in split order; output gate (attention.hpp:89-92).
-// The split maxima and sums are read one split per thread; the partial sums of
-// this thread's dimension in batches of kCombineChunk splits.
-constexpr int kCombineChunk = 16;
+// Workgroup (h, q) = blk / 4, blk % 4 owns dimensions 64 q .. 64 q + 63: its
+// four waves fetch the partial sums of interleaved splits into LDS (a wave
+// fetches few lines of freshly written partials, which is what the wait
+// costs), then wave 0 folds them in split order, one dimension per lane.
+constexpr int kCombineWGs = 32;
+constexpr int kCombineChunk = 32;   // splits per LDS round (8 per wave)
 template <class IO>
 __device__ __forceinline__ bool combine_body(const AttnArgs& a, int T, int blk, IO& io) {
-  __shared__ float c_e[256], c_l[256], c_m[4];
   io.arrive();
   io.mark(0);   // trace: stage entry
   if (!io.wait()) return false;
-  const int h = blk, d = threadIdx.x, lane = d & 63, wave = d >> 6;
-  if (h >= 8 || T < 0 || T >= a.max_ctx) return true;
-  const Raw graw = io.issue1(a.qkv, h * 512 + 256 + d);   // the output gate of dimension d
+  if (blk >= kCombineWGs || T < 0 || T >= a.max_ctx) return true;
+  const int h = blk >> 2, q = blk & 3;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int d = 64 * q + lane;
   const int Tn = T + 1;
   const int ns = (Tn + kAttnSplit - 1) / kAttnSplit;
   const int base = h * a.nsplit_max;
+  const Raw graw = io.issue1(a.qkv, h * 512 + 256 + d, wave == 0);   // the output gate of dimension d
+  float* buf = io.slot();   // [kCombineChunk splits][64 dimensions]
   float M = -__builtin_inff();
-  for (int s0 = 0; s0 < ns; s0 += 256) {
-    float mv;
-    if (!io.ld1(a.pm, a.part_st, base + min(s0 + d, ns - 1), mv)) return false;
-    M = fmaxf(M, mv);
+  if (wave == 0) {
+    for (int s0 = 0; s0 < ns; s0 += 64) {
+      float mv;
+      if (!io.ld1(a.pm, a.part_st, base + min(s0 + lane, ns - 1), mv)) return false;
+      M = fmaxf(M, xor_max<64>(mv));
+    }
   }
-  M = xor_max<64>(M);
-  if (lane == 0) c_m[wave] = M;
-  __syncthreads();
-  M = fmaxf(fmaxf(c_m[0], c_m[1]), fmaxf(c_m[2], c_m[3]));
   float L = 0.0f, ctx = 0.0f;
-  for (int s0 = 0; s0 < ns; s0 += 256) {
-    const int n = min(256, ns - s0);
-    if (d < n) {
-      float mv, lv;
-      if (!io.ld1(a.pm, a.part_st, base + s0 + d, mv) || !io.ld1(a.pl, a.part_st, base + s0 + d, lv)) return false;
-      c_e[d] = dev_expf(mv - M);
-      c_l[d] = lv;
+  constexpr int kPer = kCombineChunk / 4;
+  for (int s0 = 0; s0 < ns; s0 += kCombineChunk) {
+    const int n = min(kCombineChunk, ns - s0);
+    {   // splits s0 + wave + 4 k of this chunk
+      int ia[kPer];
+      float pa[kPer];
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) ia[k] = (base + s0 + min(wave + 4 * k, n - 1)) * 256 + d;
+      if (!io.template ldn<kPer>(a.pacc, a.part_st, ia, pa)) return false;
+#pragma unroll
+      for (int k = 0; k < kPer; ++k)
+        if (wave + 4 * k < n) buf[(wave + 4 * k) * 64 + lane] = pa[k];
     }
     __syncthreads();
-    for (int c0 = 0; c0 < n; c0 += kCombineChunk) {
-      int ia[kCombineChunk];
-      float pa[kCombineChunk];
-#pragma unroll
-      for (int c = 0; c < kCombineChunk; ++c) ia[c] = (base + s0 + min(c0 + c, n - 1)) * 256 + d;
-      if (!io.template ldn<kCombineChunk>(a.pacc, a.part_st, ia, pa)) return false;
-#pragma unroll
-      for (int c = 0; c < kCombineChunk; ++c) {
-        if (c0 + c < n) {
-          const float e = c_e[c0 + c];
-          L = L + c_l[c0 + c] * e;
-          ctx = ctx + pa[c] * e;
-        }
+    if (wave == 0) {
+      float mv, lv;
+      const int sl = base + s0 + min(lane, n - 1);
+      if (!io.ld1(a.pm, a.part_st, sl, mv) || !io.ld1(a.pl, a.part_st, sl, lv)) return false;
+      const float e = dev_expf(mv - M);   // split s0 + lane
+      for (int c = 0; c < n; ++c) {
+        const float ec = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), c));
+        const float lc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lv), c));
+        L = L + lc * ec;
+        ctx = ctx + buf[c * 64 + lane] * ec;
       }
     }
     __syncthreads();
   }
-  io.mark(1);   // trace: all split partials received
+  if (wave != 0) return true;
+  io.mark(1);   // trace: all split partials folded
   const float invL = 1.0f / L;
   float gate;
   if (!io.resolve1(graw, a.qkv, a.qkv_st, h * 512 + 256 + d, gate)) return false;
