@@ -46,7 +46,8 @@ static hipError_t launch_gemv_r(const GemvArgs& a, int grid, dim3 blk, hipStream
 
 // Rows per batch (a.rows_per_batch) must match how the segment batches were counted.
 hipError_t launch_gemv(const GemvArgs& a, int waves_per_block, hipStream_t s) {
-  if (a.nseg < 1 || a.nseg > 4 || waves_per_block < 1 || waves_per_block > 4) return hipErrorInvalidValue;
+  if (a.nseg < 1 || a.nseg > 4 || (waves_per_block != 1 && waves_per_block != 2 && waves_per_block != 4))
+    return hipErrorInvalidValue;
   if (a.prologue == P_LOADQ && a.mode != M_W8A8) return hipErrorInvalidValue;
   if (a.prologue == P_GATED && a.K != 2048) return hipErrorInvalidValue;
   const int total = a.seg[a.nseg - 1].batch0 + a.seg[a.nseg - 1].nbatch;

@@ -751,6 +751,12 @@ __device__ __forceinline__ int seg_of(const GemvArgs& a, int b) {
   return __builtin_amdgcn_readfirstlane(si);
 }
 
+// The quantised activation of a W8A8 GEMV workgroup: [NCH][64 lanes][4 dwords].
+__device__ __forceinline__ uint32_t* gemv_qlds() {
+  __shared__ __attribute__((aligned(16))) uint32_t q[4 * 64 * 4];
+  return q;
+}
+
 template <int NCH, int MODE, int PRO, int R, class IO>
 __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, IO& io, int tokv) {
   const int lane = threadIdx.x & 63, nwv = blockDim.x >> 6;
@@ -768,6 +774,9 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
   // poll of x, the weights, the epilogue inputs and the norm gains.  Waves
   // without rows load the workgroup's last batch and drop it.
   const bool stage_x = PRO != P_LOADQ && !(PRO == P_NORM && a.emb != nullptr);
+  bool has_f32 = false;   // (read before the hand-over wait)
+  for (int i = 0; i < a.nseg; ++i) has_f32 = has_f32 || a.seg[i].kind == SEG_F32;
+  has_f32 = __builtin_amdgcn_readfirstlane((int)has_f32) != 0;
   const int bq = min(b, total - 1);
   int si = seg_of(a, bq);
   typename IO::VecPoll vx;
@@ -803,7 +812,6 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
     zl = buf;
   }
   io.mark(1);   // trace: input vector in LDS
-  if (b >= total) return true;   // no rows for this wave (block 0 / wave 0 always has some)
 
   // ---------------- 2. prologue: this lane's chunks c = lane + 64 j of x
   float xv[NCH][16];     // fp32 activation (W8A16) / dequantized q*s (W8A8)
@@ -881,21 +889,52 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
       am = xor_max<64>(am);
       xs = quant_scale(am);
       const float rs = 1.0f / xs;
+      if constexpr (NCH >= 2) {
+        // Every wave needs the lane's 4 NCH packed dwords; the waves quantise
+        // them round robin and the packed bytes meet in LDS.
+        uint32_t* ql = gemv_qlds();
 #pragma unroll
-      for (int j = 0; j < NCH; ++j) {
-        int q[16];
+        for (int j = 0; j < NCH; ++j)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          q[e] = quant_one_r(xv[j][e], xs, rs);
-          xv[j][e] = (float)q[e] * xs;
+          for (int d = 0; d < 4; ++d) {
+            if (((4 * j + d) & (nwv - 1)) == wave) {   // nwv is 1, 2 or 4
+              int q[4];
+#pragma unroll
+              for (int k = 0; k < 4; ++k) q[k] = quant_one_r(xv[j][4 * d + k], xs, rs);
+              ql[(j * 64 + lane) * 4 + d] = pack4(q[0], q[1], q[2], q[3]);
+            }
+          }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) {
+          const u32x4 t = *as_lds(reinterpret_cast<const u32x4*>(ql + (j * 64 + lane) * 4));
+#pragma unroll
+          for (int d = 0; d < 4; ++d) xq[j][d] = t[d];
         }
+        if (has_f32) {   // fp32-weight segments take the dequantised activation
 #pragma unroll
-        for (int d = 0; d < 4; ++d) xq[j][d] = pack4(q[4 * d], q[4 * d + 1], q[4 * d + 2], q[4 * d + 3]);
+          for (int j = 0; j < NCH; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) xv[j][e] = i8_at(xq[j], e) * xs;
+        }
+      } else {   // one chunk per lane: every wave quantises it
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) {
+          int q[16];
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            q[e] = quant_one_r(xv[j][e], xs, rs);
+            xv[j][e] = (float)q[e] * xs;
+          }
+#pragma unroll
+          for (int d = 0; d < 4; ++d) xq[j][d] = pack4(q[4 * d], q[4 * d + 1], q[4 * d + 2], q[4 * d + 3]);
+        }
       }
     }
   }
 
   io.mark(2);   // trace: prologue done
+  if (b >= total) return true;   // no rows for this wave (it took part in the barriers above)
   const int b0 = b;
   // ---------------- 3. row batches (the next batch's loads overlap this batch's reduction)
   for (; b < total; b += stride) {
