@@ -69,6 +69,12 @@ struct qh_engine {
   size_t arena_pairs = 0;
   uint32_t tag_next = 1;         // first unused tag (the arena holds only smaller tags)
   int* abort_dev = nullptr;      // set by a hand-over wait that gave up
+  // Lane-interleaved copies of the fp32 vectors a wave reads 16 elements per
+  // lane (norm gains, the DeltaNet gate rows): element e of lane l's chunk of
+  // each 1024-element row at (e / 4) * 256 + 4 l + e % 4, so one 16-byte load
+  // instruction of a wave covers 1 KiB of consecutive memory.
+  float* lanes = nullptr;
+  int64_t lane_off[kLayers + 1][R_COUNT];   // float offset in lanes, or -1
   hipEvent_t launch_ev[2] = {};  // around the last persistent launch (engine stream)
   float last_launch_ms = 0.0f;
 };
@@ -78,6 +84,10 @@ namespace {
 const float* f32p(const qh_engine* e, int layer, Role r) {
   const Entry* en = e->L->get(layer, r);
   return reinterpret_cast<const float*>(e->blob + en->off);
+}
+const float* lanep(const qh_engine* e, int layer, Role r) {
+  const int64_t o = e->lane_off[layer][r];
+  return o < 0 ? nullptr : e->lanes + o;
 }
 const int8_t* i8p(const qh_engine* e, int layer, Role r) {
   return reinterpret_cast<const int8_t*>(e->blob + e->L->get(layer, r)->off);
@@ -158,10 +168,11 @@ void build_layers(const qh_engine* e, int l0, int l1, bool embed, Bufs& B, std::
       a.x = h.p;
       a.x_st = h.st;
       a.out_st = sA;
-      a.nw = f32p(e, l, R_IN_LN);
+      a.nw = lanep(e, l, R_IN_LN);
+      a.nw_lanes = 1;
       a.eps = kEps;
       a.done = done;
-      float* convd = B.take(kConvDim, e->convd);
+      float* convd = B.take(tag ? kConvDim + 16 * kLH : kConvDim, e->convd);   // tagged: + the gates
       float* zb = B.take(kZDim, e->zb);
       if (embed && l == l0) {   // embed_row (qwen_synth.hpp:42-43), written to the residual
         a.emb = i8p(e, kLayers, R_EMBED);
@@ -179,6 +190,13 @@ void build_layers(const qh_engine* e, int l0, int l1, bool embed, Bufs& B, std::
       a.seg[1] = mkseg(SEG_I8, E_SILU, kZDim, a.seg[0].nbatch, zb);   // silu(z) for the gated norm
       a.seg[1].w = i8p(e, l, R_Z);
       a.seg[1].sw = scp(e, l, R_Z);
+      if (tag) {   // the gates b, a of the 16 heads, from this prologue's activation
+        a.gw = lanep(e, l, R_B);   // wb rows, then the wa rows (consecutive in lanes)
+        a.grows = 2 * kLH;
+        a.g_alog = f32p(e, l, R_ALOG);
+        a.g_dtb = f32p(e, l, R_DTB);
+        a.gout = B.at(convd, kConvDim);
+      }
       out.push_back(gemv_stage(ST_GEMV_NORM_1x8, a));
       const int sB = (int)out.size();
       DnArgs d;   // gates b, a (deltanet.hpp:164-165), l2norm, delta rule (deltanet.hpp:166-173)
@@ -187,10 +205,11 @@ void build_layers(const qh_engine* e, int l0, int l1, bool embed, Bufs& B, std::
       d.gb = e->gb;
       d.gx = h.p;
       d.gx_st = h.st;
-      d.gx_norm = f32p(e, l, R_IN_LN);
+      d.gx_norm = lanep(e, l, R_IN_LN);
       d.eps = kEps;
-      d.wb = f32p(e, l, R_B);
-      d.wa = f32p(e, l, R_A);
+      d.wb = lanep(e, l, R_B);
+      d.wa = lanep(e, l, R_A);
+      d.lanes = 1;
       d.A_log = f32p(e, l, R_ALOG);
       d.dt_bias = f32p(e, l, R_DTB);
       d.mode = e->mode;
@@ -202,7 +221,7 @@ void build_layers(const qh_engine* e, int l0, int l1, bool embed, Bufs& B, std::
       d.S = e->rec + (size_t)li * kLH * kLK * kLV;
       d.o = B.take(kLH * kLV, e->o);
       d.o_st = sB;
-      if (tag) d.gt = B.take(2 * kLH, e->gb);
+      d.gates_in_convd = tag ? 1 : 0;
       d.done = done;
       Stage sd;
       sd.kind = ST_DELTANET;
@@ -240,7 +259,8 @@ void build_layers(const qh_engine* e, int l0, int l1, bool embed, Bufs& B, std::
       a.x = h.p;
       a.x_st = h.st;
       a.out_st = sA;
-      a.nw = f32p(e, l, R_IN_LN);
+      a.nw = lanep(e, l, R_IN_LN);
+      a.nw_lanes = 1;
       a.eps = kEps;
       a.done = done;
       a.nseg = 3;
@@ -311,7 +331,8 @@ void build_layers(const qh_engine* e, int l0, int l1, bool embed, Bufs& B, std::
     m.x = h.p;
     m.x_st = h.st;
     m.out_st = sD;
-    m.nw = f32p(e, l, R_POST_LN);
+    m.nw = lanep(e, l, R_POST_LN);
+    m.nw_lanes = 1;
     m.eps = kEps;
     m.done = done;
     m.nseg = 1;
@@ -349,7 +370,8 @@ Stage head_stage(const qh_engine* e, Bufs& B, const Vec& h, bool with_logits, in
   HeadArgs& hd = st.hd;
   hd.h = h.p;
   hd.h_st = h.st;
-  hd.nw = f32p(e, kLayers, R_FINAL);
+  hd.nw = lanep(e, kLayers, R_FINAL);
+  hd.nw_lanes = 1;
   hd.eps = kEps;
   hd.w = i8p(e, kLayers, R_EMBED);
   hd.sw = scp(e, kLayers, R_EMBED);
@@ -559,7 +581,7 @@ void release(qh_engine* e) {
   void* bufs[] = {e->blob, e->rec, e->conv, e->kc, e->vc, e->h, e->convd, e->zb, e->gb, e->o, e->act,
                   e->og, e->qkv, e->pm, e->pl, e->pacc, e->rope, e->logits, e->part_val,
                   e->part_idx, e->ctl, e->prompt_dev, e->out_dev, e->prog[0], e->prog[1], e->arena,
-                  e->abort_dev};
+                  e->abort_dev, e->lanes};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   for (hipEvent_t ev : e->launch_ev)
@@ -588,6 +610,31 @@ int ensure_io(qh_engine* e, int n) {
   return QH_OK;
 }
 
+// Rows of 1024 fp32 from the blob into the lane-interleaved order (see qh_engine::lanes).
+int build_lanes(qh_engine* e, const uint8_t* blob) {
+  const Role roles[] = {R_IN_LN, R_POST_LN, R_B, R_A, R_FINAL};
+  std::vector<float> host;
+  for (int l = 0; l <= kLayers; ++l)
+    for (int r = 0; r < R_COUNT; ++r) e->lane_off[l][r] = -1;
+  for (int l = 0; l <= kLayers; ++l)
+    for (Role r : roles) {
+      const Entry* en = e->L->get(l, r);
+      if (en == nullptr || en->dtype != 0 || en->numel() % 1024 != 0) continue;
+      const float* src = reinterpret_cast<const float*>(blob + en->off);
+      e->lane_off[l][r] = (int64_t)host.size();
+      const size_t rows = (size_t)(en->numel() / 1024);
+      for (size_t row = 0; row < rows; ++row) {
+        const size_t base = host.size();
+        host.resize(base + 1024);
+        for (int ln = 0; ln < 64; ++ln)
+          for (int el = 0; el < 16; ++el) host[base + (el / 4) * 256 + 4 * ln + el % 4] = src[row * 1024 + 16 * ln + el];
+      }
+    }
+  QH_TRY(dalloc(&e->lanes, host.size()));
+  QH_HIP(hipMemcpy(e->lanes, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice));
+  return QH_OK;
+}
+
 int create(const void* blob, size_t blob_len, const char* idx_text, int max_ctx, qh_engine** out) {
   if (!out) return QH_EINVAL;
   *out = nullptr;
@@ -610,6 +657,7 @@ int create(const void* blob, size_t blob_len, const char* idx_text, int max_ctx,
   QH_C(hip_status(hipStreamCreate(&e->stream)));
   QH_C(dalloc(&e->blob, blob_len));
   QH_C(hip_status(hipMemcpy(e->blob, blob, blob_len, hipMemcpyHostToDevice)));
+  QH_C(build_lanes(e, static_cast<const uint8_t*>(blob)));
   QH_C(dalloc(&e->rec, (size_t)kNLinear * kLH * kLK * kLV));
   QH_C(dalloc(&e->conv, (size_t)kNLinear * kConvDim * kConvK));
   QH_C(dalloc(&e->kc, (size_t)kNFull * max_ctx * kKVProj));

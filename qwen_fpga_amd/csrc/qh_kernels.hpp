@@ -52,6 +52,7 @@ struct GemvArgs {
   int rows_per_batch = 8;       // 4 or 8 rows reduced together per wave
   const float* x = nullptr;     // P_LOAD / P_NORM input, P_GATED o
   const float* nw = nullptr;    // P_NORM [K] gain, P_GATED [128] gain
+  int nw_lanes = 0;             // P_NORM, K = 1024: nw in the lane-interleaved order (load16c)
   const float* z = nullptr;     // P_GATED gate input [2048]
   const int8_t* xq = nullptr;   // P_LOADQ
   const float* sx = nullptr;
@@ -64,6 +65,15 @@ struct GemvArgs {
   const int* done = nullptr;    // engine stop flag (skip when *done != 0)
   int x_st = 0, z_st = 0;       // producer stages of x / z (tagged I/O)
   int out_st = 0;               // this stage: tag of every output (segments and h_out)
+  // DeltaNet gate rows (P_NORM, K = 1024; tagged in_proj): fp32 rows in the lane-interleaved
+  // order, wb (beta, rows 0..15) then wa (g, rows 16..31); row r on wave 0 of workgroup
+  // nblk - 1 - r, from the prologue's activation.  Head h's g goes to pair 16 h of gout,
+  // beta to pair 16 h + 1 (deltanet.hpp:164-165).
+  const float* gw = nullptr;
+  int grows = 0;
+  const float* g_alog = nullptr;
+  const float* g_dtb = nullptr;
+  float* gout = nullptr;
   int nseg = 0;
   Seg seg[4];
 };
@@ -72,6 +82,7 @@ struct GemvArgs {
 struct HeadArgs {
   const float* h = nullptr;     // [1024] final hidden (pre-norm)
   const float* nw = nullptr;    // final norm gain
+  int nw_lanes = 0;             // nw in the lane-interleaved order (load16c)
   float eps = 1e-6f;
   const int8_t* w = nullptr;    // [rows][1024]
   const float* sw = nullptr;
@@ -132,6 +143,7 @@ struct DnArgs {
   const float* gx = nullptr;
   const float* gx_norm = nullptr;
   float eps = 1e-6f;
+  int lanes = 0;                 // gx_norm, wb and wa rows in the lane-interleaved order (load16c)
   const float* wb = nullptr;     // fp32 [16][1024]
   const float* wa = nullptr;     // fp32 [16][1024]
   const float* A_log = nullptr;
@@ -142,8 +154,8 @@ struct DnArgs {
   int mode = M_W8A16;
   float* S = nullptr;            // [16][128][128]
   float* o = nullptr;            // [16][128]
-  float* gt = nullptr;           // tagged g[16] beta[16]: the gates, computed by workgroups of this
-                                 // stage that own no head quarter (persistent kernel; null: each unit)
+  int gates_in_convd = 0;        // tagged I/O: g and beta of head h are pairs 6144 + 16 h and
+                                 // 6144 + 16 h + 1 of convd (computed by the in_proj stage)
   int normalize = 1;             // l2norm q,k and scale q (0: given already normalized)
   int heads = 16;                // heads to process (1 for the single-head op)
   const int* done = nullptr;
@@ -168,10 +180,13 @@ enum StageKind : int {
 };
 struct Stage {
   int kind = ST_GEMV_NORM_1x8;
-  GemvArgs g;
-  DnArgs d;
-  AttnArgs at;
-  HeadArgs hd;
+  union {   // the arguments of `kind` (all members are trivially copyable)
+    GemvArgs g;
+    DnArgs d;
+    AttnArgs at;
+    HeadArgs hd;
+  };
+  Stage() : g() {}
 };
 
 // Persistent decode: prog[0..nstage) is one token (embed .. LM head).  The

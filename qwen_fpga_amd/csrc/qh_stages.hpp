@@ -68,6 +68,12 @@ __device__ __forceinline__ float* lds_ring() {
   return ring;
 }
 
+// Per-wave areas for region polls (pollr_finish): 512 floats per wave.
+__device__ __forceinline__ float* wave_area() {
+  __shared__ __attribute__((aligned(16))) float a[4 * 512];
+  return a + 512 * (threadIdx.x >> 6);
+}
+
 struct PlainIO {
   static constexpr bool kTagged = false;
   const int* done = nullptr;   // engine stop flag (graph engine); null: never stopped
@@ -154,6 +160,41 @@ struct PlainIO {
     for (int j = 0; j < N; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) v[j][e] = P.v[j][e];
+#pragma unroll
+    for (int m = 0; m < M; ++m) v1[m] = P.v1[m];
+    return true;
+  }
+  // Region poll (see TagIO): lane l reads elements 2l, 2l + 1 of each 128-element region and writes
+  // them to dst + 128 r + 2l (LDS, this wave's own area); plus M single elements.
+  template <int R, int M>
+  struct PollR {
+    float v[R][2];
+    float v1[M];
+  };
+  template <int R, int M>
+  __device__ __forceinline__ void pollr_issue(const float* base, const int (&rb)[R], const int (&idx1)[M],
+                                              PollR<R, M>& P) {
+    const int lane = threadIdx.x & 63;
+    const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const u32x2 t = __builtin_amdgcn_raw_buffer_load_b64(rs, (rb[r] + 2 * lane) * 4, 0, kSc1);
+      P.v[r][0] = __uint_as_float(t[0]);
+      P.v[r][1] = __uint_as_float(t[1]);
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) P.v1[m] = ldcb(base, idx1[m]);
+  }
+  template <int R, int M>
+  __device__ __forceinline__ bool pollr_finish(const float*, int, const int (&)[R], const int (&)[M], PollR<R, M>& P,
+                                               float* dst, float (&v1)[M]) {
+    const int lane = threadIdx.x & 63;
+    __attribute__((address_space(3))) float* d = (__attribute__((address_space(3))) float*)dst;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      d[128 * r + 2 * lane] = P.v[r][0];
+      d[128 * r + 2 * lane + 1] = P.v[r][1];
+    }
 #pragma unroll
     for (int m = 0; m < M; ++m) v1[m] = P.v1[m];
     return true;
@@ -395,6 +436,62 @@ struct TagIO {
     for (int m = 0; m < M; ++m) v1[m] = __uint_as_float(P.u1[m][0]);
     return true;
   }
+  // Region poll: R regions of 128 consecutive pairs (1 KiB each, first pair rb[r]) and M single
+  // pairs.  Lane l loads pairs 2l, 2l + 1 of every region with one 16-byte load, so a load
+  // instruction covers eight whole lines -- a wave fetches each freshly written line once (the
+  // 16-element form touches eight lines per instruction, 16 bytes of each, again and again).  The
+  // values go to dst + 128 r + 2l, this wave's own LDS area, for any lane to read back.
+  template <int R, int M>
+  struct PollR {
+    u32x4 u[R];
+    u32x2 u1[M];
+  };
+  template <int R, int M>
+  __device__ __forceinline__ void pollr_issue(const float* base, const int (&rb)[R], const int (&idx1)[M],
+                                              PollR<R, M>& P) {
+    const int lane = threadIdx.x & 63;
+    const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int r = 0; r < R; ++r) P.u[r] = __builtin_amdgcn_raw_buffer_load_b128(rs, (rb[r] + 2 * lane) * 8, 0, kSc1);
+#pragma unroll
+    for (int m = 0; m < M; ++m) P.u1[m] = __builtin_amdgcn_raw_buffer_load_b64(rs, idx1[m] * 8, 0, kSc1);
+    asm volatile("" ::: "memory");   // nothing issued later may move ahead of these loads
+  }
+  template <int R, int M>
+  __device__ __forceinline__ bool pollr_finish(const float* base, int st, const int (&rb)[R], const int (&idx1)[M],
+                                               PollR<R, M>& P, float* dst, float (&v1)[M]) {
+    const uint32_t tg = tag(st);
+    auto tags = [&]() {
+      bool ok = true;
+#pragma unroll
+      for (int r = 0; r < R; ++r) ok = ok & (P.u[r][1] == tg) & (P.u[r][3] == tg);
+#pragma unroll
+      for (int m = 0; m < M; ++m) ok = ok & (P.u1[m][1] == tg);
+      return wave_all(ok);
+    };
+    const bool hit = tags();
+    mark(3);   // trace: first poll returned
+    if (!hit) {
+      const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
+      unsigned polls = 0;
+      do {
+        if (!again(polls) || !sample(rs, idx1[M - 1], tg, polls)) return false;
+        pollr_issue<R, M>(base, rb, idx1, P);
+      } while (!tags());
+      mark(4);   // trace: complete after a repoll
+    }
+    const int lane = threadIdx.x & 63;
+    __attribute__((address_space(3))) float* d = (__attribute__((address_space(3))) float*)dst;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      d[128 * r + 2 * lane] = __uint_as_float(P.u[r][0]);
+      d[128 * r + 2 * lane + 1] = __uint_as_float(P.u[r][2]);
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) v1[m] = __uint_as_float(P.u1[m][0]);
+    return true;
+  }
   template <int N, int M>
   __device__ __forceinline__ bool ld16vn(const float* base, int st, const int (&idx)[N], float (&v)[N][16],
                                          const int (&idx1)[M], float (&v1)[M]) {
@@ -617,6 +714,27 @@ __device__ __forceinline__ void load16l(const float* p, float* v) {
     for (int e = 0; e < 4; ++e) v[4 * k + e] = t[e];
   }
 }
+// Lane l's 16-element chunk of a 1024-element fp32 row stored lane-interleaved
+// (element e at (e / 4) * 256 + 4 l + e % 4): each of the four loads of a wave
+// reads 1 KiB of consecutive memory.
+__device__ __forceinline__ void load16c(const float* row, int l, float* v) {
+  const __attribute__((address_space(1))) f32x4* q = as_global(reinterpret_cast<const f32x4*>(row));
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const f32x4 t = q[64 * k + l];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[4 * k + e] = t[e];
+  }
+}
+// load16c through a buffer descriptor (an empty one reads zeros); row_f: float offset of the row
+__device__ __forceinline__ void load16c_rs(const __amdgpu_buffer_rsrc_t& rs, int row_f, int l, float* v) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rs, (row_f + 256 * k + 4 * l) * 4, 0, 0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[4 * k + e] = __uint_as_float(t[e]);
+  }
+}
 // 16 int8 from global memory
 __device__ __forceinline__ void load16b(const int8_t* p, uint32_t* w) {
   const u32x4 t = *as_global(reinterpret_cast<const u32x4*>(p));
@@ -789,12 +907,23 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
     load_batch<NCH, R>(g, row0, K, nchunk, lane, w);   // SEG_F32: never read
     epi_prefetch(g, row0 + row_of_lane<R>(lane), aux, io);
   }
+  // a DeltaNet gate row (GemvArgs::gw), wave 0 of workgroups nblk - 1 - r
+  const int grow = nblk - 1 - blk;
+  const bool gate_wave = PRO == P_NORM && NCH == 1 && wave == 0 && grow < a.grows;
+  float gwv[16];
+  if constexpr (PRO == P_NORM && NCH == 1) {
+    const __amdgpu_buffer_rsrc_t rg = rsrc_n(a.gw, gate_wave ? 0x7ffffff0 : 0);
+    load16c_rs(rg, gate_wave ? grow * 1024 : 0, lane, gwv);
+  }
   float nwv16[NCH][16];   // norm gains: constants, loaded before the hand-over wait
   if constexpr (PRO == P_NORM || PRO == P_GATED) {
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int c = min(lane + 64 * j, nchunk - 1);
-      load16g(a.nw + (PRO == P_GATED ? ((16 * c) & 127) : 16 * c), nwv16[j]);
+      if (PRO == P_NORM && a.nw_lanes)
+        load16c(a.nw, c, nwv16[j]);   // K = 1024: c = lane
+      else
+        load16g(a.nw + (PRO == P_GATED ? ((16 * c) & 127) : 16 * c), nwv16[j]);
     }
   }
   if (!io.wait()) return false;
@@ -934,6 +1063,18 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
   }
 
   io.mark(2);   // trace: prologue done
+  if constexpr (PRO == P_NORM && NCH == 1) {
+    if (gate_wave) {   // deltanet.hpp:164-165 on the prologue's (normalised, quantised) activation
+      const int hh = grow & 15;
+      const float y = xor_sum<64>(dot16_f32(gwv, xv[0], 0.0f));
+      float val;
+      if (grow < 16)
+        val = dev_sigmoid(y);   // beta
+      else
+        val = -dev_expf(as_global(a.g_alog)[hh]) * dev_softplus(y + as_global(a.g_dtb)[hh]);   // g
+      if (lane == 0) io.st1(a.gout, a.out_st, 16 * hh + (grow < 16 ? 1 : 0), val);
+    }
+  }
   if (b >= total) return true;   // no rows for this wave (it took part in the barriers above)
   const int b0 = b;
   // ---------------- 3. row batches (the next batch's loads overlap this batch's reduction)
@@ -1065,7 +1206,10 @@ __device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, 
   head_load(a, b, total, lane, rl, w0, sc0);   // two batches in flight before the norm prologue
   head_load(a, b + stride, total, lane, rl, w1, sc1);
   float xv[16], nw[16];
-  load16g(a.nw + 16 * lane, nw);
+  if (a.nw_lanes)
+    load16c(a.nw, lane, nw);
+  else
+    load16g(a.nw + 16 * lane, nw);
   if (!io.wait()) return false;
   {
     float* hl = io.slot();
@@ -1166,7 +1310,10 @@ __device__ __forceinline__ bool deltanet_gates(const DnArgs& a, int h, int tokv,
   }
   if (a.gx_norm != nullptr) {   // norm.hpp:13-20
     float nw[16];
-    load16g(a.gx_norm + 16 * lane, nw);
+    if (a.lanes)
+      load16c(a.gx_norm, lane, nw);
+    else
+      load16g(a.gx_norm + 16 * lane, nw);
     float ss = dot16_f32(xv, xv, 0.0f);
     ss = xor_sum<64>(ss);
     const float inv = 1.0f / sqrtf(ss / 1024.0f + a.eps);
@@ -1183,44 +1330,51 @@ __device__ __forceinline__ bool deltanet_gates(const DnArgs& a, int h, int tokv,
 #pragma unroll
     for (int e = 0; e < 16; ++e) xv[e] = (float)quant_one_r(xv[e], xs, rs) * xs;
   }
-  float w[16];
-  load16g(a.wb + (size_t)h * 1024 + 16 * lane, w);
+  float w[16], w2[16];
+  if (a.lanes) {
+    load16c(a.wb + (size_t)h * 1024, lane, w);
+    load16c(a.wa + (size_t)h * 1024, lane, w2);
+  } else {
+    load16g(a.wb + (size_t)h * 1024 + 16 * lane, w);
+    load16g(a.wa + (size_t)h * 1024 + 16 * lane, w2);
+  }
   const float yb = xor_sum<64>(dot16_f32(w, xv, 0.0f));
-  load16g(a.wa + (size_t)h * 1024 + 16 * lane, w);
-  const float ya = xor_sum<64>(dot16_f32(w, xv, 0.0f));
+  const float ya = xor_sum<64>(dot16_f32(w2, xv, 0.0f));
   beta = dev_sigmoid(yb);
   g = -dev_expf(as_global(a.A_log)[h]) * dev_softplus(ya + as_global(a.dt_bias)[h]);
   return true;
 }
 
-// gates_given: g and beta come from the tagged vector a.gt (written by the
-// gate workgroups of this stage) instead of being computed by every wave.
-template <class IO>
-__device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool valid, bool gates_given, IO& io,
-                                              int tokv) {
+// GATES: g and beta are pairs 6144 + 16 h and 6144 + 16 h + 1 of the tagged
+// convd vector (written by the in_proj stage, see GemvArgs::gw) and arrive
+// with q, k and v; otherwise every wave computes them.
+template <bool GATES, class IO>
+__device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool valid, IO& io, int tokv) {
   const int h = unit / kDnVQuarters, vq = unit % kDnVQuarters;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kg = lane & 7, v = vq * 32 + 8 * wave + (lane >> 3);
   float* Sh = a.S + (size_t)h * 128 * 128;
   io.arrive();
   io.mark(0);   // trace: stage entry
-  // convd = q (2048) | k (2048) | v (2048), post-conv; chunks of this lane's k-group
-  const int idx[2] = {h * 128 + 16 * kg, 2048 + h * 128 + 16 * kg};
-  const int iv[1] = {4096 + h * 128 + v};
-  typename IO::template Poll16<2, 1> P;
+  // convd = q (2048) | k (2048) | v (2048), post-conv: the head's q and k (one 128-element region
+  // each) and the v element of this lane's column
+  constexpr int M = GATES ? 3 : 1;
+  const int reg[2] = {h * 128, 2048 + h * 128};
+  int iv[M];
+  if constexpr (GATES) {
+    iv[0] = 6144 + 16 * h;       // g
+    iv[1] = 6144 + 16 * h + 1;   // beta
+  }
+  iv[M - 1] = 4096 + h * 128 + v;   // (the poll samples the last one)
+  typename IO::template PollR<2, M> P;
   float s[16];
   float g = 0.0f, beta = 0.0f;
-  Raw rg, rb;
   if (valid) {
-    io.template poll_issue<2, 1>(a.convd, idx, iv, P);
-    if (gates_given) {
-      rg = io.issue1(a.gt, h);
-      rb = io.issue1(a.gt, 16 + h);
-    }
+    io.template pollr_issue<2, M>(a.convd, reg, iv, P);
 #pragma unroll
     for (int i = 0; i < 16; ++i) s[i] = as_global(Sh)[(kg * 16 + i) * 128 + v];
     // inputs final before in_proj: computed while the hand-over is in flight
-    if (!gates_given && a.wa != nullptr && !deltanet_gates(a, h, tokv, g, beta, io)) return false;
+    if (!GATES && a.wa != nullptr && !deltanet_gates(a, h, tokv, g, beta, io)) return false;
   }
   if (!io.wait()) return false;
   if (!valid) return true;
@@ -1230,10 +1384,15 @@ __device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool va
       beta = ldcb(a.gb, 16 + h);
     }
   }
-  float qk[2][16], vv[1];
-  if (!io.template poll_finish<2, 1>(a.convd, a.convd_st, idx, iv, P, qk, vv)) return false;
-  if (gates_given && (!io.resolve1(rg, a.gt, a.o_st, h, g) || !io.resolve1(rb, a.gt, a.o_st, 16 + h, beta)))
-    return false;
+  float qk[2][16], vv[M];
+  float* wa = wave_area();
+  if (!io.template pollr_finish<2, M>(a.convd, a.convd_st, reg, iv, P, wa, vv)) return false;
+  load16l(wa + 16 * kg, qk[0]);         // q rows 16 kg .. 16 kg + 15
+  load16l(wa + 128 + 16 * kg, qk[1]);   // k rows 16 kg .. 16 kg + 15
+  if constexpr (GATES) {
+    g = vv[0];
+    beta = vv[1];
+  }
   io.mark(1);   // trace: q, k, v of the head received
   if (a.normalize) {   // l2norm (deltanet.hpp:134); q also scaled by 1/sqrt(128) (deltanet.hpp:168-169)
 #pragma unroll
@@ -1256,7 +1415,7 @@ __device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool va
     p = p + s[i] * qk[1][i];
   }
   p = xor_sum<8>(p);
-  const float d = (vv[0] - p) * beta;
+  const float d = (vv[M - 1] - p) * beta;
   io.mark(2);   // trace: delta computed (sweep A done)
   p = 0.0f;
 #pragma unroll
@@ -1271,29 +1430,19 @@ __device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool va
 }
 
 // All heads * kDnVQuarters units; the first one of each workgroup prefetches.
-// With tagged I/O and enough workgroups, workgroups units .. units + heads - 1
-// compute the gates of one head each (wave 0) and hand them over.
+// All heads * kDnVQuarters units; the first one of each workgroup prefetches.
 template <class IO>
 __device__ __forceinline__ bool deltanet_all(const DnArgs& a, int blk, int nblk, IO& io, int tokv) {
   const int units = a.heads * kDnVQuarters;
-  const bool gate_wgs = IO::kTagged && a.gt != nullptr && a.wa != nullptr && nblk >= units + a.heads;
-  if (gate_wgs && blk >= units) {
-    io.arrive();
-    io.mark(0);   // trace: stage entry
-    const int h = blk - units;
-    if (h < a.heads && threadIdx.x < 64) {
-      float g = 0.0f, beta = 0.0f;
-      if (!deltanet_gates(a, h, tokv, g, beta, io)) return false;
-      if (threadIdx.x == 0) {
-        io.st1(a.gt, a.o_st, h, g);
-        io.st1(a.gt, a.o_st, 16 + h, beta);
-      }
-    }
-    return true;
+  if (IO::kTagged && a.gates_in_convd) {
+    if (!deltanet_body<true>(a, blk, blk < units, io, tokv)) return false;
+    for (int u = blk + nblk; u < units; u += nblk)
+      if (!deltanet_body<true>(a, u, true, io, tokv)) return false;
+  } else {
+    if (!deltanet_body<false>(a, blk, blk < units, io, tokv)) return false;
+    for (int u = blk + nblk; u < units; u += nblk)
+      if (!deltanet_body<false>(a, u, true, io, tokv)) return false;
   }
-  if (!deltanet_body(a, blk, blk < units, gate_wgs, io, tokv)) return false;
-  for (int u = blk + nblk; u < units; u += nblk)
-    if (!deltanet_body(a, u, true, gate_wgs, io, tokv)) return false;
   return true;
 }
 
