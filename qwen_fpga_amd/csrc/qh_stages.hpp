@@ -68,10 +68,11 @@ __device__ __forceinline__ float* lds_ring() {
   return ring;
 }
 
-// Per-wave areas for region polls (pollr_finish): 512 floats per wave.
+// Per-wave areas for region polls (pollr_finish): 768 floats (six regions) per wave.
+constexpr int kWaveArea = 768;
 __device__ __forceinline__ float* wave_area() {
-  __shared__ __attribute__((aligned(16))) float a[4 * 512];
-  return a + 512 * (threadIdx.x >> 6);
+  __shared__ __attribute__((aligned(16))) float a[4 * kWaveArea];
+  return a + kWaveArea * (threadIdx.x >> 6);
 }
 
 struct PlainIO {
@@ -1545,25 +1546,35 @@ __device__ __forceinline__ bool attn_unit(const AttnArgs& a, int s, int j, int T
   const int t0 = s * kAttnSplit;
   const int tl = T - t0;                    // slot T within the split (OWNER)
   // qkv = q||gate (4096, interleaved per head) | k (512) | v (512): the query
-  // (attention.hpp:40); the owner also takes the new K row and this lane's
-  // four new V elements
-  constexpr int NQ = OWNER ? 2 : 1, NV = OWNER ? 4 : 1;
-  int idx[NQ], iv[NV];
-  idx[0] = h * 512 + 16 * g16;
+  // (attention.hpp:40) as two 128-element regions; the owner also takes the
+  // new K and V rows of kv head j (two regions each)
+  constexpr int NR = OWNER ? 6 : 2;
+  int reg[NR];
+  reg[0] = h * 512;
+  reg[1] = h * 512 + 128;
   if constexpr (OWNER) {
-    idx[1] = 4096 + j * 256 + 16 * g16;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) iv[e] = 4608 + j * 256 + 4 * lane + e;
-  } else {
-    iv[0] = idx[0];   // (an element of the query chunk)
+    reg[2] = 4096 + j * 256;
+    reg[3] = 4096 + j * 256 + 128;
+    reg[4] = 4608 + j * 256;
+    reg[5] = 4608 + j * 256 + 128;
   }
-  typename IO::template Poll16<NQ, NV> P;
-  io.template poll_issue<NQ, NV>(a.qkv, idx, iv, P);
+  const int iv[1] = {h * 512 + lane};   // (sampled while waiting: a query element)
+  typename IO::template PollR<NR, 1> P;
+  io.template pollr_issue<NR, 1>(a.qkv, reg, iv, P);
   AttnPre pf;
   attn_prefetch(a, s, j, T, rrow, pf);
   if (!io.wait()) return false;
-  float t2[NQ][16], vT[NV];
-  if (!io.template poll_finish<NQ, NV>(a.qkv, a.qkv_st, idx, iv, P, t2, vT)) return false;
+  float* wa = wave_area();
+  float unused[1];
+  if (!io.template pollr_finish<NR, 1>(a.qkv, a.qkv_st, reg, iv, P, wa, unused)) return false;
+  float t2[OWNER ? 2 : 1][16], vT[4];
+  load16l(wa + 16 * g16, t2[0]);   // query dims 16 g16 .. + 15
+  if constexpr (OWNER) {
+    load16l(wa + 256 + 16 * g16, t2[1]);   // new K row, same dims
+    const f32x4 t = *as_lds(reinterpret_cast<const f32x4*>(wa + 512 + 4 * lane));   // new V row, dims 4 lane ..
+#pragma unroll
+    for (int e = 0; e < 4; ++e) vT[e] = t[e];
+  }
   io.mark(1);   // trace: q (and the new k, v) received
   if constexpr (OWNER) {
     qk_norm_rope(t2[1], pf.kn, a.eps, g16, pf.cs, pf.sn);
