@@ -912,9 +912,17 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
   const int grow = nblk - 1 - blk;
   const bool gate_wave = PRO == P_NORM && NCH == 1 && wave == 0 && grow < a.grows;
   float gwv[16];
+  float g_alog = 0.0f, g_dtb = 0.0f;   // the head's A_log and dt_bias (g rows only)
   if constexpr (PRO == P_NORM && NCH == 1) {
     const __amdgpu_buffer_rsrc_t rg = rsrc_n(a.gw, gate_wave ? 0x7ffffff0 : 0);
     load16c_rs(rg, gate_wave ? grow * 1024 : 0, lane, gwv);
+    // constants: loaded with the gate row, ahead of the hand-over wait (empty
+    // descriptors read 0 on waves that compute no g)
+    const bool g_row = gate_wave && grow >= 16;
+    g_alog = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc_n(a.g_alog, g_row ? 64 : 0),
+                                                                           4 * (grow & 15), 0, 0));
+    g_dtb = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc_n(a.g_dtb, g_row ? 64 : 0),
+                                                                          4 * (grow & 15), 0, 0));
   }
   float nwv16[NCH][16];   // norm gains: constants, loaded before the hand-over wait
   if constexpr (PRO == P_NORM || PRO == P_GATED) {
@@ -1072,7 +1080,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
       if (grow < 16)
         val = dev_sigmoid(y);   // beta
       else
-        val = -dev_expf(as_global(a.g_alog)[hh]) * dev_softplus(y + as_global(a.g_dtb)[hh]);   // g
+        val = -dev_expf(g_alog) * dev_softplus(y + g_dtb);   // g
       if (lane == 0) io.st1(a.gout, a.out_st, 16 * hh + (grow < 16 ? 1 : 0), val);
     }
   }
