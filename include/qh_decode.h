@@ -137,6 +137,14 @@ int qh_mlp_layer(float* out, const float* x, const qh_tensor* gate_w, const qh_t
  * per-vector symmetric int8: s = amax/127 (1 if amax == 0), q = rint(x/s) clipped to +-127.
  *                          golden/model.py:37-45 _qa; scripts/export_gemv_tv.py:25-30 q_i8_vec */
 int qh_quant_act(int8_t* xq, float* sx, const float* x, int n, void* stream);
+/* ---- offline weight quantisation (the packer of scripts/pack_weights.py:79-86) ----
+ * per output row of w[rows][cols]: s = amax/127 (1 if amax == 0), q = rint(w/s) clipped to
+ * +-127, fp32 arithmetic, round half to even.        golden/quant.py:43-49 quant_rows
+ * A row holding a NaN or an infinity gets scale NaN and q = 0 (the reference leaves it
+ * undefined).  _bf16 takes the raw bfloat16 bits of a safetensors tensor and widens them
+ * exactly (golden/loader.py:34-38 _bf16_to_f32). */
+int qh_quant_rows(int8_t* q, float* scale, const float* w, int rows, int cols, void* stream);
+int qh_quant_rows_bf16(int8_t* q, float* scale, const uint16_t* w, int rows, int cols, void* stream);
 /* acc[o] = sum_i w[o,i]*xq[i] in int32; y[o] = float(acc[o]) * sx * scale[o]
  * (acc may be NULL)              rtl/gemv_i8.sv:52-72; scripts/export_gemv_tv.py:49-50 */
 int qh_gemv_i8_w8a8(float* y, int32_t* acc, const int8_t* w, const float* scale, const int8_t* xq,

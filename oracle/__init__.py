@@ -86,6 +86,7 @@ def lib():
         _sig(L, "or_delta_rule_layer", None, [P, P, P, P, P, P, P])
         _sig(L, "or_quant_act", None, [P, P, P, I])
         _sig(L, "or_quant_act_markstein", None, [P, P, P, I])
+        _sig(L, "or_quant_rows", None, [P, P, P, I, I])
         _sig(L, "or_dev_gemv_i8", None, [P, P, P, P, I, I])
         _sig(L, "or_dev_gemv_f32", None, [P, P, P, I, I])
         _sig(L, "or_dev_rmsnorm", None, [P, P, P, I, F])
@@ -110,6 +111,16 @@ def lib():
         _OR = L
     return _OR
 
+
+
+def quant_rows(w: np.ndarray):
+    """quant.py:43-49 quant_rows of an fp32 [rows, cols] array: (int8 q, fp32 scale)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    q = np.empty((rows, cols), np.int8)
+    s = np.empty(rows, np.float32)
+    lib().or_quant_rows(q.ctypes.data, s.ctypes.data, w.ctypes.data, rows, cols)
+    return q, s
 
 def ref():
     """The compiled reference kernels, or None if oracle/_ref was not built."""

@@ -425,6 +425,27 @@ void or_quant_act(int8_t* q, float* s, const float* x, int n) {
   *s = sc;
 }
 
+/* quant.py:43-49 quant_rows, the offline weight quantizer of pack_weights.py:
+ * per output row amax = max|w|, s = amax/127 (1 if amax == 0), q = rint(w/s)
+ * clipped to +-127, all in fp32 (numpy float32 division, round half to even):
+ * per row exactly or_quant_act.  A row holding a NaN or an infinity has no
+ * defined result in the reference (numpy casts NaN to int8); here, as on the
+ * device, its scale is NaN and its q are 0, so a packer can reject it. */
+void or_quant_rows(int8_t* q, float* s, const float* w, int rows, int cols) {
+  for (int r = 0; r < rows; ++r) {
+    const float* wr = w + (long)r * cols;
+    int8_t* qr = q + (long)r * cols;
+    int finite = 1;
+    for (int i = 0; i < cols; ++i) finite &= isfinite(wr[i]) ? 1 : 0;
+    if (!finite) {
+      memset(qr, 0, (size_t)cols);
+      s[r] = NAN;
+      continue;
+    }
+    or_quant_act(qr, &s[r], wr, cols);
+  }
+}
+
 void or_gemv_w8a8(float* y, int32_t* acc, const int8_t* w, const float* sw, const int8_t* xq, float sx,
                   int out, int in) {
 #pragma omp parallel for num_threads(g_threads) schedule(static)

@@ -251,6 +251,16 @@ def gemv_i8_w8a8(y, acc, w, scale, xq, sx, out: int, in_: int, stream=None):
     _call("qh_gemv_i8_w8a8", y, acc, w, scale, xq, sx, out, in_, _Ptr(_stream(stream)))
 
 
+def quant_rows(q, scale, w, rows: int, cols: int, stream=None):
+    """golden/quant.py:43-49 quant_rows on the device: per row s = amax/127 (1 if 0),
+    q = rint(w/s) clipped to +-127.  ``w`` is fp32 [rows, cols] or the raw bits of a
+    bfloat16 tensor (torch.bfloat16 / int16 / uint16), widened exactly on the device;
+    q is int8 [rows, cols], scale fp32 [rows].  A row with a non-finite value gets
+    scale NaN and q = 0."""
+    bits16 = str(getattr(w, "dtype", "")).rsplit(".", 1)[-1] in ("bfloat16", "int16", "uint16")
+    _call("qh_quant_rows_bf16" if bits16 else "qh_quant_rows", q, scale, w, rows, cols, _Ptr(_stream(stream)))
+
+
 # ---------------------------------------------------------------- layout / synthetic weights
 
 def blob_size() -> int:

@@ -276,6 +276,102 @@ hipError_t launch_quant(int8_t* q, float* sx, const float* x, int n, hipStream_t
   return hipGetLastError();
 }
 
+// Offline per-row weight quantisation (quant.py:43-49 quant_rows, used by
+// pack_weights.py:79-86): one wave per row.  A row of up to kQRowRegs * 256
+// elements with cols % 4 == 0 and aligned pointers is read once into
+// registers (fp32: 16-byte loads; bf16 bits: 8-byte loads widened exactly by a
+// 16-bit shift), its amax taken with the xor tree (max is exact in any order),
+// and written as one dword of four int8 per lane and chunk; other rows take
+// two passes over memory.  s = amax/127 (1 if amax == 0) and the quotient
+// RN(w/s) is Markstein's correction from rs = RN(1/s), exact on |w| <= amax.
+// A row holding a NaN or an infinity gets scale NaN and q = 0.
+constexpr int kQRowRegs = 16;
+__device__ __forceinline__ float qr_widen(float v) { return v; }
+__device__ __forceinline__ float qr_widen(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
+__device__ __forceinline__ void qr_load4(const float* p, float (&v)[4]) {
+  const f32x4 t = *as_global(reinterpret_cast<const f32x4*>(p));
+  v[0] = t[0];
+  v[1] = t[1];
+  v[2] = t[2];
+  v[3] = t[3];
+}
+__device__ __forceinline__ void qr_load4(const uint16_t* p, float (&v)[4]) {
+  const u32x2 t = *as_global(reinterpret_cast<const u32x2*>(p));
+  v[0] = __uint_as_float(t[0] << 16);
+  v[1] = __uint_as_float(t[0] & 0xffff0000u);
+  v[2] = __uint_as_float(t[1] << 16);
+  v[3] = __uint_as_float(t[1] & 0xffff0000u);
+}
+template <typename T>
+__global__ __launch_bounds__(256) void quant_rows_kernel(int8_t* q, float* scale, const T* w, int rows, int cols,
+                                                         int vec) {
+  const int lane = threadIdx.x & 63;
+  const int row = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (row >= rows) return;   // whole waves: no barrier follows
+  const T* wr = w + (size_t)row * cols;
+  int8_t* qr = q + (size_t)row * cols;
+  float am = 0.0f;
+  bool bad = false;
+  if (vec) {   // cols % 4 == 0, cols <= kQRowRegs * 256, aligned
+    float v[kQRowRegs][4];
+#pragma unroll
+    for (int c = 0; c < kQRowRegs; ++c) {
+      const int i = 4 * (lane + 64 * c);
+      if (i < cols) {
+        qr_load4(wr + i, v[c]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float a = fabsf(v[c][k]);
+          bad = bad || !(a <= 3.402823466e38f);
+          am = fmaxf(am, a);
+        }
+      }
+    }
+    am = xor_max<64>(am);
+    bad = !wave_all(!bad);
+    const float s = bad ? __builtin_nanf("") : quant_scale(am);
+    const float rs = 1.0f / s;
+#pragma unroll
+    for (int c = 0; c < kQRowRegs; ++c) {
+      const int i = 4 * (lane + 64 * c);
+      if (i < cols) {
+        int t[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) t[k] = bad ? 0 : quant_one_r(v[c][k], s, rs);
+        *as_global_w(reinterpret_cast<uint32_t*>(qr + i)) = pack4(t[0], t[1], t[2], t[3]);
+      }
+    }
+    if (lane == 0) scale[row] = s;
+    return;
+  }
+  for (int i = lane; i < cols; i += 64) {
+    const float a = fabsf(qr_widen(wr[i]));
+    bad = bad || !(a <= 3.402823466e38f);
+    am = fmaxf(am, a);
+  }
+  am = xor_max<64>(am);
+  bad = !wave_all(!bad);
+  const float s = bad ? __builtin_nanf("") : quant_scale(am);
+  const float rs = 1.0f / s;
+  for (int i = lane; i < cols; i += 64) qr[i] = bad ? (int8_t)0 : (int8_t)quant_one_r(qr_widen(wr[i]), s, rs);
+  if (lane == 0) scale[row] = s;
+}
+template <typename T>
+hipError_t launch_quant_rows_t(int8_t* q, float* scale, const T* w, int rows, int cols, hipStream_t s) {
+  if (rows <= 0 || cols <= 0) return hipErrorInvalidValue;
+  const size_t in_align = sizeof(T) == 4 ? 16 : 8;
+  const int vec = cols % 4 == 0 && cols <= kQRowRegs * 256 && reinterpret_cast<uintptr_t>(w) % in_align == 0 &&
+                  reinterpret_cast<uintptr_t>(q) % 4 == 0;
+  quant_rows_kernel<T><<<(rows + 3) / 4, 256, 0, s>>>(q, scale, w, rows, cols, vec);
+  return hipGetLastError();
+}
+hipError_t launch_quant_rows(int8_t* q, float* scale, const float* w, int rows, int cols, hipStream_t s) {
+  return launch_quant_rows_t(q, scale, w, rows, cols, s);
+}
+hipError_t launch_quant_rows_bf16(int8_t* q, float* scale, const uint16_t* w, int rows, int cols, hipStream_t s) {
+  return launch_quant_rows_t(q, scale, w, rows, cols, s);
+}
+
 __global__ void set_ints_kernel(int* dst, int a, int b) {
   dst[0] = a;
   dst[1] = b;

@@ -233,6 +233,8 @@ hipError_t launch_conv1d(float* out, const float* in, float* state, const float*
                          hipStream_t s);
 hipError_t launch_apply_rope(float* x, const float* cs, const float* sn, hipStream_t s);
 hipError_t launch_quant(int8_t* q, float* sx, const float* x, int n, hipStream_t s);
+hipError_t launch_quant_rows(int8_t* q, float* scale, const float* w, int rows, int cols, hipStream_t s);
+hipError_t launch_quant_rows_bf16(int8_t* q, float* scale, const uint16_t* w, int rows, int cols, hipStream_t s);
 hipError_t launch_set_ints(int* dst, int a, int b, hipStream_t s);
 hipError_t launch_set_int(int* dst, int v, hipStream_t s);
 hipError_t launch_store_gb(float* gb, float g, float beta, hipStream_t s);

@@ -452,6 +452,16 @@ int qh_quant_act(int8_t* xq, float* sx, const float* x, int n, void* stream) {
   return hip_status(launch_quant(xq, sx, x, n, S(stream)));
 }
 
+int qh_quant_rows(int8_t* q, float* scale, const float* w, int rows, int cols, void* stream) {
+  if (!q || !scale || !w || rows <= 0 || cols <= 0) return QH_EINVAL;
+  return hip_status(launch_quant_rows(q, scale, w, rows, cols, S(stream)));
+}
+
+int qh_quant_rows_bf16(int8_t* q, float* scale, const uint16_t* w, int rows, int cols, void* stream) {
+  if (!q || !scale || !w || rows <= 0 || cols <= 0) return QH_EINVAL;
+  return hip_status(launch_quant_rows_bf16(q, scale, w, rows, cols, S(stream)));
+}
+
 int qh_gemv_i8_w8a8(float* y, int32_t* acc, const int8_t* w, const float* scale, const int8_t* xq,
                     const float* sx, int out, int in, void* stream) {
   if (!y || !w || !scale || !xq || !sx || !aligned16(w) || !aligned16(xq)) return QH_EINVAL;

@@ -890,8 +890,8 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
   if (blk * nwv >= total) return true;   // no rows for this workgroup (workgroup-uniform)
   // ---------------- 1. the first poll of x, then weights and epilogue inputs of the first batch
   // One straight-line block issues every load of the first batch: the first
-  // poll of x, the weights, the epilogue inputs and the norm gains.  Waves
-  // without rows load the workgroup's last batch and drop it.
+  // poll of x, the norm gains, the gate row, the weights and the epilogue
+  // inputs.  Waves without rows load the workgroup's last batch and drop it.
   const bool stage_x = PRO != P_LOADQ && !(PRO == P_NORM && a.emb != nullptr);
   bool has_f32 = false;   // (read before the hand-over wait)
   for (int i = 0; i < a.nseg; ++i) has_f32 = has_f32 || a.seg[i].kind == SEG_F32;
@@ -902,11 +902,16 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
   if constexpr (PRO != P_LOADQ) io.stage_issue(a.x, stage_x ? K : 0, vx);
   uint32_t w[NCH][R][4];
   EpiAux aux;
-  {
-    const Seg& g = a.seg[si];
-    const int row0 = (bq - g.batch0) * R;
-    load_batch<NCH, R>(g, row0, K, nchunk, lane, w);   // SEG_F32: never read
-    epi_prefetch(g, row0 + row_of_lane<R>(lane), aux, io);
+  float nwv16[NCH][16];   // norm gains: constants, loaded before the hand-over wait
+  if constexpr (PRO == P_NORM || PRO == P_GATED) {
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = min(lane + 64 * j, nchunk - 1);
+      if (PRO == P_NORM && a.nw_lanes)
+        load16c(a.nw, c, nwv16[j]);   // K = 1024: c = lane
+      else
+        load16g(a.nw + (PRO == P_GATED ? ((16 * c) & 127) : 16 * c), nwv16[j]);
+    }
   }
   // a DeltaNet gate row (GemvArgs::gw), wave 0 of workgroups nblk - 1 - r
   const int grow = nblk - 1 - blk;
@@ -924,16 +929,14 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
     g_dtb = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc_n(a.g_dtb, g_row ? 64 : 0),
                                                                           4 * (grow & 15), 0, 0));
   }
-  float nwv16[NCH][16];   // norm gains: constants, loaded before the hand-over wait
-  if constexpr (PRO == P_NORM || PRO == P_GATED) {
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int c = min(lane + 64 * j, nchunk - 1);
-      if (PRO == P_NORM && a.nw_lanes)
-        load16c(a.nw, c, nwv16[j]);   // K = 1024: c = lane
-      else
-        load16g(a.nw + (PRO == P_GATED ? ((16 * c) & 127) : 16 * c), nwv16[j]);
-    }
+  // The weights and epilogue inputs come last: a wave's loads return in issue
+  // order, so whatever the prologue reads (x, the norm gains, the gate row)
+  // is issued before them and its wait does not include the weights.
+  {
+    const Seg& g = a.seg[si];
+    const int row0 = (bq - g.batch0) * R;
+    load_batch<NCH, R>(g, row0, K, nchunk, lane, w);   // SEG_F32: never read
+    epi_prefetch(g, row0 + row_of_lane<R>(lane), aux, io);
   }
   if (!io.wait()) return false;
   // the workgroup's copy of x (and z): every wave takes part, rows or not
@@ -967,7 +970,11 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
     }
   } else {
     if (PRO == P_NORM && a.emb != nullptr) {   // embed_row (gemv.hpp:76-84)
-      const int tok = a.tok != nullptr ? ldc_i(a.tok) : tokv;
+      // wave-uniform at once: the wait for the token load then sits here, on
+      // this path only (consumed under the lane condition below, the load stayed
+      // pending where the paths join and the compiler drained every load there,
+      // the weights included)
+      const int tok = __builtin_amdgcn_readfirstlane(a.tok != nullptr ? ldc_i(a.tok) : tokv);
       const int8_t* er = a.emb + (size_t)tok * K;
       const float es = as_global(a.emb_s)[tok];
 #pragma unroll
