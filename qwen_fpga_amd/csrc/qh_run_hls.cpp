@@ -1,7 +1,10 @@
 // run_hls drop-in on the MI355X engine (reference CLI: hls/tb/run_hls.cpp:37-79).
 //
-//   qh_run_hls <bin> <ids.txt> <n_new> [eos] [--w8a8] [--idx weights.idx]
+//   qh_run_hls <bin> <ids.txt> <n_new> [eos] [--w8a8] [--graph] [--idx weights.idx]
 //
+// Tokens run in the persistent kernel (one launch for the prompt, one for the
+// generation) unless --graph asks for a graph launch per token or the device
+// refuses cooperative launches; both give the same ids.
 // Greedy generation from the packed int8 blob: the prompt ids are fed through
 // the recurrent path, then up to n_new ids are generated, stopping before eos.
 // Generated ids go to stdout (space separated), timing to stderr.  Exit code 2
@@ -19,9 +22,12 @@ int main(int argc, char** argv) {
   std::vector<const char*> pos;
   const char* idx = nullptr;
   int mode = QH_MODE_W8A16;
+  bool graph = false;
   for (int i = 1; i < argc; ++i) {
     if (std::strcmp(argv[i], "--w8a8") == 0) {
       mode = QH_MODE_W8A8;
+    } else if (std::strcmp(argv[i], "--graph") == 0) {
+      graph = true;
     } else if (std::strcmp(argv[i], "--idx") == 0 && i + 1 < argc) {
       idx = argv[++i];
     } else {
@@ -29,7 +35,7 @@ int main(int argc, char** argv) {
     }
   }
   if (pos.size() < 3) {
-    std::fprintf(stderr, "usage: qh_run_hls <bin> <ids.txt> <n_new> [eos] [--w8a8] [--idx weights.idx]\n");
+    std::fprintf(stderr, "usage: qh_run_hls <bin> <ids.txt> <n_new> [eos] [--w8a8] [--graph] [--idx weights.idx]\n");
     return 2;
   }
   const int n_new = std::atoi(pos[2]);
@@ -55,6 +61,7 @@ int main(int argc, char** argv) {
     return st == QH_EIO || st == QH_EFORMAT ? 2 : 1;
   }
   qh_engine_set_mode(e, mode);
+  if (!graph) (void)qh_engine_set_exec(e, QH_EXEC_PERSISTENT);   // QH_ESTATE: no cooperative launch
   using clk = std::chrono::steady_clock;
   auto ms = [](clk::time_point a, clk::time_point b) {
     return std::chrono::duration<double, std::milli>(b - a).count();

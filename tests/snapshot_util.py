@@ -88,3 +88,32 @@ def make_snapshot(d: str, seed: int = 0, sparse: bool = False) -> dict:
     tensors.append(("mtp.fc.weight", "BF16", (4, 8), lambda: bf16_bits(rng, 32, 119).astype("<u2").tobytes()))
     write_safetensors(os.path.join(d, "model.safetensors"), tensors, sparse=sparse)
     return man
+
+
+IM_START, IM_END = 248045, 248046   # chat markers; IM_END is the eos
+
+
+def write_tokenizer(d: str) -> None:
+    """A word-level tokenizer over all 248,320 ids, saved like a checkpoint's
+    (tokenizer.json + tokenizer_config.json with a chat template): "hello" = 1,
+    "world" = 2, "user" = 3, "assistant" = 4, the chat markers at 248045/248046,
+    every other id a word "w<id>"; words are split on whitespace and decoding
+    joins them with spaces."""
+    from tokenizers import Tokenizer
+    from tokenizers.models import WordLevel
+    from tokenizers.pre_tokenizers import WhitespaceSplit
+    from transformers import PreTrainedTokenizerFast
+
+    vocab = {f"w{i}": i for i in range(248320)}
+    special = {"<unk>": 0, "hello": 1, "world": 2, "user": 3, "assistant": 4, "<|im_start|>": IM_START,
+               "<|im_end|>": IM_END}
+    for w, i in special.items():
+        vocab.pop(f"w{i}")
+        vocab[w] = i
+    tk = Tokenizer(WordLevel(vocab, unk_token="<unk>"))
+    tk.pre_tokenizer = WhitespaceSplit()
+    chat = ("{% for m in messages %}<|im_start|> {{ m['role'] }} {{ m['content'] }} <|im_end|> {% endfor %}"
+            "{% if add_generation_prompt %}<|im_start|> assistant {% endif %}")
+    fast = PreTrainedTokenizerFast(tokenizer_object=tk, unk_token="<unk>", eos_token="<|im_end|>")
+    fast.chat_template = chat
+    fast.save_pretrained(d)

@@ -165,3 +165,31 @@ def test_tb_decode_on_packed_blob(orc, packed):
     r = subprocess.run([os.path.join(ROOT, "qwen_fpga_amd", "bin", "qh_tb_decode"), packed["blob"], packed["idx"], ref],
                        capture_output=True, text=True, timeout=180)
     assert r.returncode == 0 and "PASS" in r.stdout, r.stdout + r.stderr
+
+
+def test_run_hls_wrapper_on_packed_snapshot(q, packed, tmp_path, capsys):
+    """run_hls.py's flow: tokenizer from the snapshot, blob packed on first use, qh_run_hls spawned."""
+    from transformers import AutoTokenizer
+
+    from qwen_fpga_amd import run_hls
+    from snapshot_util import IM_END, IM_START, write_tokenizer
+
+    write_tokenizer(packed["snap"])
+    tok = AutoTokenizer.from_pretrained(packed["snap"])
+    fresh = str(tmp_path / "artifacts")   # no blob yet: the wrapper packs it
+    for raw, art, ids in ((True, os.path.dirname(packed["blob"]), [1, 2]),
+                          (False, fresh, [IM_START, 3, 1, 2, IM_END, IM_START, 4])):
+        rc = run_hls.main(["-p", "hello world", "-n", "6", "--snapshot", packed["snap"], "--artifacts", art]
+                          + (["--raw"] if raw else []))
+        out = capsys.readouterr().out
+        assert rc == 0, out
+        with open(os.path.join(art, "prompt_ids.txt")) as f:
+            assert f.read() == " ".join(map(str, ids))
+        e = q.Engine(path=packed["blob"], idx=packed["idx"], max_ctx=32)
+        try:
+            gen = e.generate(ids, 6, eos=IM_END)
+        finally:
+            e.close()
+        assert out.split("answer   : ", 1)[1].split("\n", 1)[0] == tok.decode(gen)
+    with open(os.path.join(fresh, "qwen35_int8.bin"), "rb") as f, open(packed["blob"], "rb") as g:
+        assert f.read() == g.read()
