@@ -87,6 +87,7 @@ def lib():
         _sig(L, "or_quant_act", None, [P, P, P, I])
         _sig(L, "or_quant_act_markstein", None, [P, P, P, I])
         _sig(L, "or_quant_rows", None, [P, P, P, I, I])
+        _sig(L, "or_matvec_fixed", None, [P, P, P, P, P, I, I, I, I])
         _sig(L, "or_dev_gemv_i8", None, [P, P, P, P, I, I])
         _sig(L, "or_dev_gemv_f32", None, [P, P, P, I, I])
         _sig(L, "or_dev_rmsnorm", None, [P, P, P, I, F])
@@ -121,6 +122,20 @@ def quant_rows(w: np.ndarray):
     s = np.empty(rows, np.float32)
     lib().or_quant_rows(q.ctypes.data, s.ctypes.data, w.ctypes.data, rows, cols)
     return q, s
+
+
+def matvec_fixed(w: np.ndarray, xq: np.ndarray, mult: np.ndarray, shift: int = 16, outw: int = 16):
+    """rtl/matvec_i8.sv on int8 w [out, in], int8 xq [in], int32 mult [out]: (y_q int32, acc int32)."""
+    w = np.ascontiguousarray(w, dtype=np.int8)
+    xq = np.ascontiguousarray(xq, dtype=np.int8)
+    mult = np.ascontiguousarray(mult, dtype=np.int32)
+    out, in_ = w.shape
+    yq = np.empty(out, np.int32)
+    acc = np.empty(out, np.int32)
+    lib().or_matvec_fixed(yq.ctypes.data, acc.ctypes.data, w.ctypes.data, mult.ctypes.data, xq.ctypes.data, out,
+                          in_, shift, outw)
+    return yq, acc
+
 
 def ref():
     """The compiled reference kernels, or None if oracle/_ref was not built."""

@@ -88,6 +88,9 @@ void or_quant_act(int8_t* q, float* s, const float* x, int n);
 /* quant.py:43-49 quant_rows: per row or_quant_act; a row with a non-finite
  * value gets scale NaN and q = 0 (undefined in the reference) */
 void or_quant_rows(int8_t* q, float* s, const float* w, int rows, int cols);
+/* rtl/matvec_i8.sv: int32 acc, then dequant.sv's (acc*mult + 2^(shift-1)) >>> shift in outw bits */
+void or_matvec_fixed(int32_t* yq, int32_t* acc, const int8_t* w, const int32_t* mult, const int8_t* xq, int out,
+                     int in, int shift, int outw);
 /* export_gemv_tv.py:298-299: exact int32 acc, y = float(acc) * sx * sw */
 void or_gemv_w8a8(float* y, int32_t* acc, const int8_t* w, const float* sw, const int8_t* xq, float sx,
                   int out, int in);

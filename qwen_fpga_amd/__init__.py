@@ -251,6 +251,19 @@ def gemv_i8_w8a8(y, acc, w, scale, xq, sx, out: int, in_: int, stream=None):
     _call("qh_gemv_i8_w8a8", y, acc, w, scale, xq, sx, out, in_, _Ptr(_stream(stream)))
 
 
+def matvec_i8(y_q, acc, w, mult, xq, out: int, in_: int, shift: int = 16, outw: int = 16, stream=None):
+    """rtl/matvec_i8.sv: int32 acc = w @ xq, y_q = (acc*mult + 2^(shift-1)) >>> shift in outw bits."""
+    _call("qh_matvec_i8", y_q, acc, w, mult, xq, out, in_, shift, outw, _Ptr(_stream(stream)))
+
+
+def dequant_mult(sx: float, sw, outq: int = 14, shift: int = 16) -> np.ndarray:
+    """Host-side fixed-point multipliers llround(sx*sw[o]*2^(outq+shift)) (rtl/tb/sim_matvec.cpp:36-41)."""
+    sw = np.ascontiguousarray(sw, dtype=np.float32)
+    mult = np.empty(sw.size, np.int32)
+    _call("qh_dequant_mult", mult, float(sx), sw, int(sw.size), outq, shift)
+    return mult
+
+
 def quant_rows(q, scale, w, rows: int, cols: int, stream=None):
     """golden/quant.py:43-49 quant_rows on the device: per row s = amax/127 (1 if 0),
     q = rint(w/s) clipped to +-127.  ``w`` is fp32 [rows, cols] or the raw bits of a

@@ -20,6 +20,7 @@ enum Epi : int {
   E_SWIGLU = 5,  // pair rows (gate i, up i): out[i] = silu(g)*u (mlp.hpp:17)
   E_ACC = 6,     // out[row] = y and acc_out[row] = int32 accumulator (W8A8 op)
   E_SILU = 7,    // out[row] = silu(y)  (the gated norm's silu(z), norm.hpp:32)
+  E_ACCI = 8,    // acc_out[row] = int32 accumulator only (the RTL's gemv_i8; sw may be null)
 };
 enum Prologue : int {
   P_LOAD = 0,    // x[K] fp32 as given
@@ -233,6 +234,8 @@ hipError_t launch_conv1d(float* out, const float* in, float* state, const float*
                          hipStream_t s);
 hipError_t launch_apply_rope(float* x, const float* cs, const float* sn, hipStream_t s);
 hipError_t launch_quant(int8_t* q, float* sx, const float* x, int n, hipStream_t s);
+hipError_t launch_fixed_dequant(int32_t* yq, const int32_t* acc, const int32_t* mult, int n, int shift, int outw,
+                                hipStream_t s);
 hipError_t launch_quant_rows(int8_t* q, float* scale, const float* w, int rows, int cols, hipStream_t s);
 hipError_t launch_quant_rows_bf16(int8_t* q, float* scale, const uint16_t* w, int rows, int cols, hipStream_t s);
 hipError_t launch_set_ints(int* dst, int a, int b, hipStream_t s);

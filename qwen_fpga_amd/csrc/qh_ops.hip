@@ -478,6 +478,35 @@ int qh_gemv_i8_w8a8(float* y, int32_t* acc, const int8_t* w, const float* scale,
   return hip_status(launch_gemv(a, 4, S(stream)));
 }
 
+int qh_matvec_i8(int32_t* y_q, int32_t* acc, const int8_t* w, const int32_t* mult, const int8_t* xq, int out,
+                 int in, int shift, int outw, void* stream) {
+  if (!y_q || !acc || !w || !mult || !xq || !aligned16(w) || !aligned16(xq)) return QH_EINVAL;
+  if (shift < 1 || shift > 62 || outw < 1 || outw > 32) return QH_EINVAL;
+  QH_TRY(check_gemv_shape(out, in));
+  GemvArgs a;   // gemv_i8.sv: exact int32 accumulators, no scales
+  a.K = in;
+  a.mode = M_W8A8;
+  a.prologue = P_LOADQ;
+  a.xq = xq;
+  a.nseg = 1;
+  a.seg[0] = seg_i8(w, nullptr, out, 0, nullptr, E_ACCI);
+  a.seg[0].acc_out = acc;
+  hipStream_t s = S(stream);
+  QH_HIP(launch_gemv(a, 4, s));
+  return hip_status(launch_fixed_dequant(y_q, acc, mult, out, shift, outw, s));   // dequant.sv
+}
+
+int qh_dequant_mult(int32_t* mult, float sx, const float* sw, int out, int outq, int shift) {
+  if (!mult || !sw || out <= 0 || shift < 1 || shift > 62 || outq < 0 || outq + shift > 62) return QH_EINVAL;
+  const double f = std::ldexp(1.0, outq + shift);
+  for (int o = 0; o < out; ++o) {   // sim_matvec.cpp:37-40, in double, half away from zero
+    const double c = (double)sx * (double)sw[o] * f;
+    if (!(std::fabs(c) < 2147483647.5)) return QH_ERANGE;   // would not fit the 32-bit mult port
+    mult[o] = (int32_t)std::llround(c);
+  }
+  return QH_OK;
+}
+
 // ---- layout / synthetic weights ----
 size_t qh_blob_size(void) { return (size_t)canonical_layout().total; }
 

@@ -764,7 +764,7 @@ __device__ __forceinline__ void epi_prefetch(const Seg& g, int myrow, EpiAux& x,
   const bool pair = g.kind == SEG_PAIR;
   // the row's scale: lanes of a pair segment take even rows (gate) from sw and
   // odd rows (up) from sw2, so both are loaded through uniform descriptors
-  const int i8n = g.kind == SEG_F32 ? 0 : kBig;
+  const int i8n = (g.kind == SEG_F32 || g.sw == nullptr) ? 0 : kBig;   // no scales: E_ACCI
   const int si = (pair ? (r >> 1) : r) * 4;
   const float sa = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_n(g.sw, i8n), si, 0, 0));
   const float sb = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_n(g.sw2, pair ? kBig : 0), si, 0, 0));
@@ -810,6 +810,9 @@ __device__ __forceinline__ void gemv_epilogue(const Seg& g, int ost, int lane, i
       break;
     case E_ACC:
       io.st1(g.out, ost, myrow, y);
+      as_global_w(g.acc_out)[myrow] = acci;
+      break;
+    case E_ACCI:
       as_global_w(g.acc_out)[myrow] = acci;
       break;
     case E_GATE_B:
@@ -959,7 +962,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
   uint32_t xq[NCH][4];   // int8 activation (W8A8)
   float xs = 1.0f;       // activation scale (W8A8)
   if constexpr (PRO == P_LOADQ) {
-    xs = *as_global(a.sx);
+    xs = a.sx != nullptr ? *as_global(a.sx) : 1.0f;   // E_ACCI needs no scale
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int c = lane + 64 * j;

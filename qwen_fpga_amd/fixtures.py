@@ -12,9 +12,18 @@ replay on the MI355X engine / op ABI.
   S_out [16][128][128], one after another, 2,130,048 bytes.  The reference
   passes at max |d| < 2e-5 on o_core and S_out (tb_deltanet.cpp:88-91).
 
-The same checks are the ``qh_tb_decode`` / ``qh_tb_deltanet`` programs in
-``qwen_fpga_amd/bin``.
+* ``tv_gemv.bin`` + ``tv_gemv.json`` (scripts/export_gemv_tv.py:62-72, read by
+  rtl/tb/sim_gemv.cpp and sim_matvec.cpp): int8 x[IN], int8 w[OUT][IN], int32
+  acc[OUT], float32 sx, float32 sw[OUT], float32 y[OUT] (y = float(acc)*sx*sw),
+  with {"IN": 1024, "OUT": 512} in the json.  sim_gemv passes when every
+  accumulator matches exactly; sim_matvec when the fixed-point output (SHIFT 16,
+  OUTQ 14) is within 4 LSB of round(y * 2^14) (sim_matvec.cpp:78-86).
+
+The same checks are the ``qh_tb_decode`` / ``qh_tb_deltanet`` / ``qh_sim_matvec``
+programs in ``qwen_fpga_amd/bin``.
 """
+import json
+import os
 from dataclasses import dataclass
 
 import numpy as np
@@ -27,6 +36,7 @@ TV_SHAPES = {"q": (H, K), "k": (H, K), "v": (H, V), "g": (H,), "beta": (H,), "S_
 TV_BYTES = 4 * sum(int(np.prod(s)) for s in TV_SHAPES.values())   # 2,130,048
 DECODE_TOL = 5e-2   # step-0 logits, max |d| (tb_decode.cpp:109)
 DELTA_TOL = 2e-5    # delta rule output and state, max |d| (tb_deltanet.cpp:89)
+MATVEC_LSB_TOL = 4  # fixed-point output vs round(y * 2^OUTQ) (sim_matvec.cpp:82)
 
 
 @dataclass
@@ -82,6 +92,58 @@ def write_tv_deltanet(path: str, tv: dict) -> None:
             if a.shape != TV_SHAPES[name]:
                 raise ValueError(f"{name}: shape {a.shape}, expected {TV_SHAPES[name]}")
             f.write(a.tobytes())
+
+
+@dataclass
+class GemvTv:
+    x: np.ndarray      # int8 [IN]
+    w: np.ndarray      # int8 [OUT, IN]
+    acc: np.ndarray    # int32 [OUT]
+    sx: float
+    sw: np.ndarray     # float32 [OUT]
+    y: np.ndarray      # float32 [OUT]
+
+
+def read_tv_gemv(path: str) -> GemvTv:
+    """tv_gemv.bin with its dimensions from the tv_gemv.json beside it (1024 x 512 without one)."""
+    jpath = os.path.splitext(path)[0] + ".json"
+    dims = {"IN": 1024, "OUT": 512}
+    if os.path.exists(jpath):
+        with open(jpath) as f:
+            dims = json.load(f)
+    n_in, n_out = int(dims["IN"]), int(dims["OUT"])
+    raw = np.fromfile(path, dtype=np.uint8)
+    need = n_in + n_out * n_in + 4 * n_out + 4 + 8 * n_out
+    if raw.size != need:
+        raise ValueError(f"{path}: {raw.size} bytes, IN={n_in} OUT={n_out} needs {need}")
+    o = 0
+
+    def take(n, dt):
+        nonlocal o
+        a = raw[o:o + n * np.dtype(dt).itemsize].view(dt)
+        o += n * np.dtype(dt).itemsize
+        return a
+
+    x = take(n_in, "<i1").astype(np.int8)
+    w = take(n_out * n_in, "<i1").astype(np.int8).reshape(n_out, n_in)
+    acc = take(n_out, "<i4").astype(np.int32)
+    sx = float(take(1, "<f4")[0])
+    sw = take(n_out, "<f4").astype(np.float32)
+    y = take(n_out, "<f4").astype(np.float32)
+    return GemvTv(x, w, acc, sx, sw, y)
+
+
+def write_tv_gemv(path: str, tv: GemvTv) -> None:
+    n_out, n_in = tv.w.shape
+    with open(path, "wb") as f:
+        np.asarray(tv.x, "<i1").tofile(f)
+        np.asarray(tv.w, "<i1").reshape(-1).tofile(f)
+        np.asarray(tv.acc, "<i4").tofile(f)
+        np.array([tv.sx], "<f4").tofile(f)
+        np.asarray(tv.sw, "<f4").tofile(f)
+        np.asarray(tv.y, "<f4").tofile(f)
+    with open(os.path.splitext(path)[0] + ".json", "w") as f:
+        json.dump({"IN": n_in, "OUT": n_out}, f)
 
 
 def replay_decode_ref(engine, ref: DecodeRef) -> dict:
