@@ -71,7 +71,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build runs batch-1 decode on a single MI355X "
-              "(multi-GPU is design-only, see DESIGN.md)", file=sys.stderr)
+              "(the independent unit is a whole sequence: one engine per GPU, no exchange)", file=sys.stderr)
         return 2
 
     import numpy as np

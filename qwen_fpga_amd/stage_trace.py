@@ -1,6 +1,6 @@
 """Per-stage timing of the persistent decode kernel (needs a GPU).
 
-    python -m qwen_fpga_amd.stage_trace [--pos 305] [--mode w8a8|w8a16] [--out FILE]
+    python -m qwen_fpga_amd.stage_trace [--pos 305] [--mode w8a8|w8a16] [--out stage_trace.txt]
 
 Builds the seeded synthetic model, generates greedily up to position ``pos``,
 then decodes a few more tokens with ``QH_TRACE_FILE`` set: ``persist_kernel``
@@ -85,7 +85,7 @@ def main(argv=None) -> None:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--pos", type=int, default=305)
     ap.add_argument("--mode", choices=("w8a8", "w8a16"), default="w8a8")
-    ap.add_argument("--out", default="gpurun_out/stage_trace.txt")
+    ap.add_argument("--out", default="stage_trace.txt")
     ap.add_argument("--summarise-only", action="store_true", help="summarise an existing trace file")
     args = ap.parse_args(argv)
     if not args.summarise_only:
