@@ -42,7 +42,12 @@ extern "C" {
 #define QH_EFORMAT (-4)  /* weight index or blob does not match the layout  */
 #define QH_ENOMEM (-5)   /* host or device allocation failed                */
 #define QH_ESTATE (-6)   /* engine not in a state that allows the call      */
-#define QH_EDEVICE (-7)  /* a device-side wait timed out (grid barrier)      */
+#define QH_EDEVICE (-7)  /* a hand-over wait of the persistent kernel gave up:
+                            every workgroup left the launch; the engine refuses to
+                            decode (QH_ESTATE) until qh_engine_reset.  The environment
+                            variable QH_POLL_LIMIT, read at engine creation, sets the
+                            failed polls a wait allows (default 2^20, about a second):
+                            a test hook that forces this path. */
 
 /* ---- model dimensions (hls/src/types.hpp:20-44) ----------------------- */
 #define QH_HIDDEN 1024
@@ -62,6 +67,9 @@ extern "C" {
 #define QH_KV_PROJ 512
 #define QH_ROPE_DIM 64
 #define QH_N_TENSORS 320 /* entries in weights.idx    */
+/* Largest KV context (engine max_ctx, attention T + 1): one layer's cache,
+ * 2 KiB per token, is addressed with 32-bit byte offsets. */
+#define QH_MAX_CTX 1048575
 
 /* activation precision of the engine's / layer ops' projections */
 #define QH_MODE_W8A16 0  /* int8 weights x fp32 activations (hls/src csim semantics) */
@@ -124,7 +132,8 @@ int qh_deltanet_layer(float* out, const float* x, const qh_tensor* qkv_w, const 
                       const qh_tensor* out_w, float* rec, float* conv_state, void* stream);
 /* gated GQA attention decode step                            attention.hpp:25-95 attention_layer
  * kcache/vcache hold T past tokens as [T][512]; slot T is written; attends over T+1.
- * Unlike the reference (sc[8192]) any T up to the caller's buffer is accepted. */
+ * Unlike the reference (sc[8192]) any T < QH_MAX_CTX within the caller's buffer is
+ * accepted (QH_ERANGE beyond). */
 int qh_attention_layer(float* out, const float* x, const qh_tensor* q_w, const qh_tensor* k_w,
                        const qh_tensor* v_w, const qh_tensor* o_w, const float* q_norm,
                        const float* k_norm, int pos, float* kcache, float* vcache, int T,
@@ -201,7 +210,8 @@ typedef struct qh_engine qh_engine;
 
 /* mmap `blob_path` (run_hls.cpp:27-35) and upload it; `idx_path` (may be NULL)
  * is a weights.idx whose every line must equal the canonical layout
- * (tb_decode.cpp:47-65).  max_ctx bounds the KV cache (tokens, >= 1). */
+ * (tb_decode.cpp:47-65).  max_ctx bounds the KV cache (tokens, 1 .. QH_MAX_CTX;
+ * outside that range QH_ERANGE). */
 int qh_engine_create(const char* blob_path, const char* idx_path, int max_ctx, qh_engine** out);
 /* Same from a host buffer (copied to the device; the caller may free it). */
 int qh_engine_create_from_memory(const void* blob, size_t blob_len, const char* idx_text,
@@ -210,8 +220,9 @@ int qh_engine_destroy(qh_engine* e);
 /* QH_MODE_W8A16 (default) or QH_MODE_W8A8. */
 int qh_engine_set_mode(qh_engine* e, int mode);
 /* How decode_token / generate run a token; both are bit-identical.
- * QH_EXEC_PERSISTENT: one cooperative launch per call runs every token, stage
- * after stage, with grid barriers in between.  QH_EXEC_GRAPH (default): one
+ * QH_EXEC_PERSISTENT: one cooperative launch per call runs every token; the
+ * workgroups hand each stage's outputs to the next stage's consumers through
+ * tagged buffers (no grid barrier).  QH_EXEC_GRAPH (default): one
  * replayed hipGraph of per-stage kernels per token.  No counterpart in the reference (its top is one HLS
  * function); returns QH_ESTATE if the device cannot run the persistent kernel.
  * If a cooperative launch is refused at run time (another process can hold the

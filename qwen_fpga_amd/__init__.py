@@ -63,11 +63,14 @@ class Tensor(ctypes.Structure):
     @staticmethod
     def i8(w, scale) -> "Tensor":
         out, inn = int(w.shape[0]), int(w.shape[1])
+        _dev(w, "i8", out * inn, "Tensor.i8 w")
+        _dev(scale, "f32", out, "Tensor.i8 scale")
         return Tensor(_ptr(w), _ptr(scale), None, out, inn)
 
     @staticmethod
     def f32(w) -> "Tensor":
         out, inn = int(w.shape[0]), int(w.shape[1])
+        _dev(w, "f32", out * inn, "Tensor.f32 w")
         return Tensor(None, None, _ptr(w), out, inn)
 
 
@@ -132,6 +135,29 @@ def _ptr(t) -> Optional[int]:
     raise TypeError(f"cannot pass {type(t)} as a pointer")
 
 
+_DTYPES = {"f32": ("float32",), "i8": ("int8",), "i32": ("int32",), "bf16": ("bfloat16", "int16", "uint16")}
+
+
+def _dev(t, kind: str, n: int, what: str):
+    """Checks a device-pointer argument before it reaches a kernel: a contiguous torch CUDA
+    tensor of the expected dtype holding at least n elements (a host array or a short buffer
+    would otherwise become a GPU page fault).  A _Ptr is a raw device address the caller
+    vouches for and is passed unchecked; sizes and NULL pointers are the C ABI's to reject."""
+    if t is None or isinstance(t, _Ptr):   # NULL: the C ABI rejects it where it is required
+        return t
+    if not hasattr(t, "is_cuda"):
+        raise TypeError(f"{what}: expected a torch CUDA tensor, got {type(t).__name__}")
+    if not t.is_cuda:
+        raise TypeError(f"{what}: tensor is on {t.device}, not on the GPU")
+    if str(t.dtype).rsplit(".", 1)[-1] not in _DTYPES[kind]:
+        raise TypeError(f"{what}: dtype {t.dtype}, expected {'/'.join(_DTYPES[kind])}")
+    if not t.is_contiguous():
+        raise ValueError(f"{what}: tensor is not contiguous")
+    if t.numel() < n:
+        raise ValueError(f"{what}: {t.numel()} elements, the call needs {n}")
+    return t
+
+
 def _stream(stream) -> Optional[int]:
     if stream is None:
         try:
@@ -176,84 +202,110 @@ def _call(name: str, *args) -> None:
 
 
 # ---------------------------------------------------------------- op level
-# Integer sizes are passed as plain ints; pointers must be torch CUDA tensors.
+# Integer sizes are passed as plain ints; pointers must be contiguous torch CUDA
+# tensors of the right dtype and size (checked by _dev before the call).
 
 def gemv_i8(y, w, scale, x, out: int, in_: int, stream=None):
-    _call("qh_gemv_i8", y, w, scale, x, out, in_, _Ptr(_stream(stream)))
+    _call("qh_gemv_i8", _dev(y, "f32", out, "y"), _dev(w, "i8", out * in_, "w"), _dev(scale, "f32", out, "scale"),
+          _dev(x, "f32", in_, "x"), out, in_, _Ptr(_stream(stream)))
 
 
 def gemv_f32(y, w, x, out: int, in_: int, stream=None):
-    _call("qh_gemv_f32", y, w, x, out, in_, _Ptr(_stream(stream)))
+    _call("qh_gemv_f32", _dev(y, "f32", out, "y"), _dev(w, "f32", out * in_, "w"), _dev(x, "f32", in_, "x"),
+          out, in_, _Ptr(_stream(stream)))
 
 
 def row_dot_i8(result, w, scale, h, row: int, in_: int, stream=None):
-    _call("qh_row_dot_i8", result, w, scale, h, row, in_, _Ptr(_stream(stream)))
+    _call("qh_row_dot_i8", _dev(result, "f32", 1, "result"), _dev(w, "i8", (row + 1) * in_, "w"),
+          _dev(scale, "f32", row + 1, "scale"), _dev(h, "f32", in_, "h"), row, in_, _Ptr(_stream(stream)))
 
 
 def embed_row(h, w, scale, tok: int, in_: int, stream=None):
-    _call("qh_embed_row", h, w, scale, tok, in_, _Ptr(_stream(stream)))
+    _call("qh_embed_row", _dev(h, "f32", in_, "h"), _dev(w, "i8", (tok + 1) * in_, "w"),
+          _dev(scale, "f32", tok + 1, "scale"), tok, in_, _Ptr(_stream(stream)))
 
 
 def rmsnorm(y, x, w, n: int, eps: float = EPS, stream=None):
-    _call("qh_rmsnorm", y, x, w, n, float(eps), _Ptr(_stream(stream)))
+    _call("qh_rmsnorm", _dev(y, "f32", n, "y"), _dev(x, "f32", n, "x"), _dev(w, "f32", n, "w"), n, float(eps),
+          _Ptr(_stream(stream)))
 
 
 def rmsnorm_gated(y, x, w, z, n: int, eps: float = EPS, stream=None):
-    _call("qh_rmsnorm_gated", y, x, w, z, n, float(eps), _Ptr(_stream(stream)))
+    _call("qh_rmsnorm_gated", _dev(y, "f32", n, "y"), _dev(x, "f32", n, "x"), _dev(w, "f32", n, "w"),
+          _dev(z, "f32", n, "z"), n, float(eps), _Ptr(_stream(stream)))
 
 
 def conv1d_step(out, in_ch, state, weight, stream=None):
-    _call("qh_conv1d_step", out, in_ch, state, weight, _Ptr(_stream(stream)))
+    _call("qh_conv1d_step", _dev(out, "f32", CONV_DIM, "out"), _dev(in_ch, "f32", CONV_DIM, "in_ch"),
+          _dev(state, "f32", CONV_DIM * 4, "state"), _dev(weight, "f32", CONV_DIM * 4, "weight"),
+          _Ptr(_stream(stream)))
 
 
 def rope_cos_sin(pos: int, cos_o, sin_o, stream=None):
-    _call("qh_rope_cos_sin", pos, cos_o, sin_o, _Ptr(_stream(stream)))
+    _call("qh_rope_cos_sin", pos, _dev(cos_o, "f32", 64, "cos"), _dev(sin_o, "f32", 64, "sin"),
+          _Ptr(_stream(stream)))
 
 
 def apply_rope(x, cos_, sin_, stream=None):
-    _call("qh_apply_rope", x, cos_, sin_, _Ptr(_stream(stream)))
+    _call("qh_apply_rope", _dev(x, "f32", 256, "x"), _dev(cos_, "f32", 64, "cos"), _dev(sin_, "f32", 64, "sin"),
+          _Ptr(_stream(stream)))
 
 
 def l2norm(v, n: int, stream=None):
-    _call("qh_l2norm", v, n, _Ptr(_stream(stream)))
+    _call("qh_l2norm", _dev(v, "f32", n, "v"), n, _Ptr(_stream(stream)))
 
 
 def delta_rule_head(q, k, v, g: float, beta: float, S, out, stream=None):
-    _call("qh_delta_rule_head", q, k, v, float(g), float(beta), S, out, _Ptr(_stream(stream)))
+    _call("qh_delta_rule_head", _dev(q, "f32", 128, "q"), _dev(k, "f32", 128, "k"), _dev(v, "f32", 128, "v"),
+          float(g), float(beta), _dev(S, "f32", 128 * 128, "S"), _dev(out, "f32", 128, "out"),
+          _Ptr(_stream(stream)))
 
 
 def delta_rule_layer(q, k, v, g, beta, S, out, stream=None):
-    _call("qh_delta_rule_layer", q, k, v, g, beta, S, out, _Ptr(_stream(stream)))
+    _call("qh_delta_rule_layer", _dev(q, "f32", 2048, "q"), _dev(k, "f32", 2048, "k"), _dev(v, "f32", 2048, "v"),
+          _dev(g, "f32", 16, "g"), _dev(beta, "f32", 16, "beta"), _dev(S, "f32", 16 * 128 * 128, "S"),
+          _dev(out, "f32", 2048, "out"), _Ptr(_stream(stream)))
 
 
 def deltanet_layer(out, x, qkv_w: Tensor, z_w: Tensor, b_w: Tensor, a_w: Tensor, conv_w, A_log, dt_bias,
                    gate_norm_w, out_w: Tensor, rec, conv_state, w8a8: bool = False, stream=None):
-    _call("qh_deltanet_layer_w8a8" if w8a8 else "qh_deltanet_layer", out, x, qkv_w, z_w, b_w, a_w, conv_w,
-          A_log, dt_bias, gate_norm_w, out_w, rec, conv_state, _Ptr(_stream(stream)))
+    _call("qh_deltanet_layer_w8a8" if w8a8 else "qh_deltanet_layer", _dev(out, "f32", HIDDEN, "out"),
+          _dev(x, "f32", HIDDEN, "x"), qkv_w, z_w, b_w, a_w, _dev(conv_w, "f32", CONV_DIM * 4, "conv_w"),
+          _dev(A_log, "f32", 16, "A_log"), _dev(dt_bias, "f32", 16, "dt_bias"),
+          _dev(gate_norm_w, "f32", 128, "gate_norm_w"), out_w, _dev(rec, "f32", 16 * 128 * 128, "rec"),
+          _dev(conv_state, "f32", CONV_DIM * 4, "conv_state"), _Ptr(_stream(stream)))
 
 
 def attention_layer(out, x, q_w: Tensor, k_w: Tensor, v_w: Tensor, o_w: Tensor, q_norm, k_norm, pos: int,
                     kcache, vcache, T: int, w8a8: bool = False, stream=None):
-    _call("qh_attention_layer_w8a8" if w8a8 else "qh_attention_layer", out, x, q_w, k_w, v_w, o_w, q_norm,
-          k_norm, pos, kcache, vcache, T, _Ptr(_stream(stream)))
+    n_kv = (max(T, 0) + 1) * 512
+    _call("qh_attention_layer_w8a8" if w8a8 else "qh_attention_layer", _dev(out, "f32", HIDDEN, "out"),
+          _dev(x, "f32", HIDDEN, "x"), q_w, k_w, v_w, o_w, _dev(q_norm, "f32", 256, "q_norm"),
+          _dev(k_norm, "f32", 256, "k_norm"), pos, _dev(kcache, "f32", n_kv, "kcache"),
+          _dev(vcache, "f32", n_kv, "vcache"), T, _Ptr(_stream(stream)))
 
 
 def mlp_layer(out, x, gate_w: Tensor, up_w: Tensor, down_w: Tensor, w8a8: bool = False, stream=None):
-    _call("qh_mlp_layer_w8a8" if w8a8 else "qh_mlp_layer", out, x, gate_w, up_w, down_w,
-          _Ptr(_stream(stream)))
+    _call("qh_mlp_layer_w8a8" if w8a8 else "qh_mlp_layer", _dev(out, "f32", HIDDEN, "out"),
+          _dev(x, "f32", HIDDEN, "x"), gate_w, up_w, down_w, _Ptr(_stream(stream)))
 
 
 def quant_act(xq, sx, x, n: int, stream=None):
-    _call("qh_quant_act", xq, sx, x, n, _Ptr(_stream(stream)))
+    _call("qh_quant_act", _dev(xq, "i8", n, "xq"), _dev(sx, "f32", 1, "sx"), _dev(x, "f32", n, "x"), n,
+          _Ptr(_stream(stream)))
 
 
 def gemv_i8_w8a8(y, acc, w, scale, xq, sx, out: int, in_: int, stream=None):
-    _call("qh_gemv_i8_w8a8", y, acc, w, scale, xq, sx, out, in_, _Ptr(_stream(stream)))
+    _call("qh_gemv_i8_w8a8", _dev(y, "f32", out, "y"), _dev(acc, "i32", out, "acc"),
+          _dev(w, "i8", out * in_, "w"), _dev(scale, "f32", out, "scale"), _dev(xq, "i8", in_, "xq"),
+          _dev(sx, "f32", 1, "sx"), out, in_, _Ptr(_stream(stream)))
 
 
 def matvec_i8(y_q, acc, w, mult, xq, out: int, in_: int, shift: int = 16, outw: int = 16, stream=None):
     """rtl/matvec_i8.sv: int32 acc = w @ xq, y_q = (acc*mult + 2^(shift-1)) >>> shift in outw bits."""
-    _call("qh_matvec_i8", y_q, acc, w, mult, xq, out, in_, shift, outw, _Ptr(_stream(stream)))
+    _call("qh_matvec_i8", _dev(y_q, "i32", out, "y_q"), _dev(acc, "i32", out, "acc"),
+          _dev(w, "i8", out * in_, "w"), _dev(mult, "i32", out, "mult"), _dev(xq, "i8", in_, "xq"), out, in_,
+          shift, outw, _Ptr(_stream(stream)))
 
 
 def dequant_mult(sx: float, sw, outq: int = 14, shift: int = 16) -> np.ndarray:
@@ -271,7 +323,9 @@ def quant_rows(q, scale, w, rows: int, cols: int, stream=None):
     q is int8 [rows, cols], scale fp32 [rows].  A row with a non-finite value gets
     scale NaN and q = 0."""
     bits16 = str(getattr(w, "dtype", "")).rsplit(".", 1)[-1] in ("bfloat16", "int16", "uint16")
-    _call("qh_quant_rows_bf16" if bits16 else "qh_quant_rows", q, scale, w, rows, cols, _Ptr(_stream(stream)))
+    _call("qh_quant_rows_bf16" if bits16 else "qh_quant_rows", _dev(q, "i8", rows * cols, "q"),
+          _dev(scale, "f32", rows, "scale"), _dev(w, "bf16" if bits16 else "f32", rows * cols, "w"), rows, cols,
+          _Ptr(_stream(stream)))
 
 
 # ---------------------------------------------------------------- layout / synthetic weights

@@ -77,6 +77,8 @@ struct qh_engine {
   int64_t lane_off[kLayers + 1][R_COUNT];   // float offset in lanes, or -1
   hipEvent_t launch_ev[2] = {};  // around the last persistent launch (engine stream)
   float last_launch_ms = 0.0f;
+  unsigned poll_limit = 1u << 20;  // failed polls before a hand-over wait gives up (QH_POLL_LIMIT)
+  bool broken = false;             // a launch returned QH_EDEVICE: decode refused until reset
 };
 
 namespace {
@@ -493,6 +495,7 @@ int run_persist(qh_engine* e, int tok0, int n_prompt, int n_new, int eos, bool w
   a.out_ids = e->out_dev;
   a.logits = with_logits ? e->logits : nullptr;
   a.abort_flag = e->abort_dev;
+  a.poll_limit = e->poll_limit;
   QH_HIP(hipEventRecord(e->launch_ev[0], s));
   if (launch_persist(a, e->persist_grid, s) != hipSuccess) {
     (void)hipGetLastError();
@@ -531,9 +534,12 @@ int run_persist(qh_engine* e, int tok0, int n_prompt, int n_new, int eos, bool w
     }
   }
   QH_HIP(hipEventElapsedTime(&e->last_launch_ms, e->launch_ev[0], e->launch_ev[1]));
+  if (out->err == 3 || aborted != 0) {   // state and position are undefined until a reset
+    e->broken = true;
+    return QH_EDEVICE;
+  }
   e->host_pos = out->pos;
   e->last_argmax = out->argmax;
-  if (out->err == 3 || aborted != 0) return QH_EDEVICE;
   return QH_OK;
 }
 
@@ -635,10 +641,15 @@ int build_lanes(qh_engine* e, const uint8_t* blob) {
   return QH_OK;
 }
 
+// The KV cache of one attention layer ([max_ctx][512] fp32, 2 KiB per token) is
+// addressed with 32-bit byte offsets through one buffer descriptor.
+static_assert((long long)QH_MAX_CTX * kKVProj * 4 <= 0x7ffffff0LL, "cache slice beyond one descriptor");
+
 int create(const void* blob, size_t blob_len, const char* idx_text, int max_ctx, qh_engine** out) {
   if (!out) return QH_EINVAL;
   *out = nullptr;
-  if (!blob || max_ctx < 1) return QH_EINVAL;
+  if (!blob) return QH_EINVAL;
+  if (max_ctx < 1 || max_ctx > QH_MAX_CTX) return QH_ERANGE;
   const Layout& L = canonical_layout();
   if (blob_len != L.total) return QH_EFORMAT;
   if (idx_text && !check_idx_text(idx_text, L).empty()) return QH_EFORMAT;
@@ -646,6 +657,10 @@ int create(const void* blob, size_t blob_len, const char* idx_text, int max_ctx,
   if (!e) return QH_ENOMEM;
   e->L = &L;
   e->max_ctx = max_ctx;
+  if (const char* pl = std::getenv("QH_POLL_LIMIT")) {   // test hook: force a hand-over wait to give up
+    const long v = std::strtol(pl, nullptr, 10);
+    if (v >= 0 && v <= (1L << 20)) e->poll_limit = (unsigned)v;
+  }
   e->nsplit_max = (max_ctx + kAttnSplit - 1) / kAttnSplit;
   e->head_grid = kVocab / (kRowsPerBatch * 4 * 4);   // 4 waves x 4 batches per block
   int st = QH_OK;
@@ -773,11 +788,13 @@ int qh_engine_reset(qh_engine* e) {
   QH_HIP(hipStreamSynchronize(s));
   e->host_pos = 0;
   e->last_argmax = -1;
+  e->broken = false;
   return QH_OK;
 }
 
 int qh_decode_token(qh_engine* e, int tok, float* logits, int* argmax_out) {
   if (!e || !argmax_out) return QH_EINVAL;
+  if (e->broken) return QH_ESTATE;
   if (tok < 0 || tok >= kVocab) return QH_ERANGE;
   if (e->host_pos >= e->max_ctx) return QH_ERANGE;
   if (e->exec == QH_EXEC_PERSISTENT) {   // one token = a prompt of one, no new tokens
@@ -809,6 +826,7 @@ int qh_decode_token(qh_engine* e, int tok, float* logits, int* argmax_out) {
 
 int qh_generate(qh_engine* e, const int* prompt, int n_prompt, int n_new, int eos, int* out_ids, int* n_out) {
   if (!e || !prompt || n_prompt < 1 || n_new < 0 || (n_new > 0 && !out_ids) || !n_out) return QH_EINVAL;
+  if (e->broken) return QH_ESTATE;
   for (int i = 0; i < n_prompt; ++i)
     if (prompt[i] < 0 || prompt[i] >= kVocab) return QH_ERANGE;
   if ((long)e->host_pos + n_prompt + n_new > e->max_ctx) return QH_ERANGE;
@@ -849,6 +867,7 @@ float qh_engine_last_launch_ms(const qh_engine* e) { return e ? e->last_launch_m
 
 int qh_engine_forward_layers(qh_engine* e, int l0, int l1, float* h) {
   if (!e || !h || l0 < 0 || l1 > kLayers || l0 >= l1) return QH_EINVAL;
+  if (e->broken) return QH_ESTATE;
   if (e->host_pos >= e->max_ctx) return QH_ERANGE;
   hipStream_t s = e->stream;
   QH_HIP(launch_set_int(&e->ctl->done, 0, s));
@@ -863,6 +882,7 @@ int qh_engine_forward_layers(qh_engine* e, int l0, int l1, float* h) {
 
 int qh_engine_profile(qh_engine* e, int n_steps, float* step_ms, float* head_ms) {
   if (!e || n_steps < 1 || !step_ms || !head_ms) return QH_EINVAL;
+  if (e->broken) return QH_ESTATE;
   if ((long)e->host_pos + n_steps > e->max_ctx) return QH_ERANGE;
   hipStream_t s = e->stream;
   hipEvent_t a = nullptr, b = nullptr, h0 = nullptr, h1 = nullptr;

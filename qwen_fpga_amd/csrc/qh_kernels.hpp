@@ -205,6 +205,7 @@ struct PersistArgs {
   int* out_ids = nullptr;       // [n_new]
   float* logits = nullptr;      // optional: logits of every step (the last one remains)
   int* abort_flag = nullptr;    // set when a hand-over wait exceeds its poll limit
+  unsigned poll_limit = 1u << 20;   // failed polls before a wait gives up (about a second)
   uint64_t* trace = nullptr;    // optional [trace_tokens][nstage][grid][kTraceSlots]: stage marks and end
   int trace_tokens = 0;
 };

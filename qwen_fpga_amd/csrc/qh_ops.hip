@@ -149,7 +149,7 @@ int attention_layer(float* out, const float* x, const qh_tensor* q_w, const qh_t
                     const qh_tensor* v_w, const qh_tensor* o_w, const float* q_norm, const float* k_norm,
                     int pos, float* kcache, float* vcache, int T, int mode, hipStream_t s) {
   if (!out || !x || !q_norm || !k_norm || !kcache || !vcache) return QH_EINVAL;
-  if (T < 0 || pos < 0) return QH_ERANGE;
+  if (T < 0 || pos < 0 || T >= QH_MAX_CTX) return QH_ERANGE;
   if (!tensor_i8(q_w, kQProj, kHidden) || !tensor_i8(k_w, kKVProj, kHidden) ||
       !tensor_i8(v_w, kKVProj, kHidden) || !tensor_i8(o_w, kHidden, kNH * kHD))
     return QH_EINVAL;

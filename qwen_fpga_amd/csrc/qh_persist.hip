@@ -3,9 +3,10 @@
 // bookkeeping (run_hls.cpp:56-66).  There is no grid barrier: workgroups hand
 // vectors to one another through tagged buffers (TagIO in qh_stages.hpp), so
 // each one waits only for the inputs of its own next work item.  A workgroup
-// that finishes a stage issues the next stage's weight (and own-state) loads
-// at once and then polls for that stage's inputs: HBM streaming overlaps the
-// hand-over latency.
+// that finishes a stage at once issues the next stage's first input poll and,
+// right behind it, that stage's weight (and own-state) loads: the weights
+// stream while the hand-over is awaited, and since a wave's loads return in
+// issue order, the poll is never queued behind them.
 //
 // Every stage writes its own buffers (the engine gives each stage of the
 // token program distinct output vectors), so within a token no buffer is
@@ -28,15 +29,25 @@ namespace qh {
 constexpr int kStageWords = (int)(sizeof(Stage) / 4);
 static_assert(sizeof(Stage) % 4 == 0 && kStageWords <= kPersistThreads, "one descriptor word per thread");
 
+// A wave that gave up a hand-over wait (TagIO::failed) finishes its stage with
+// stale values; at the next stage boundary it raises the workgroup's failure
+// flag in LDS, and after the boundary barrier every wave reads it and the
+// workgroup leaves the launch as one -- no wave dispatches a stage whose
+// descriptor an exited wave did not copy.  The flag is double-buffered like
+// the descriptors: slot p is written before the barrier of a boundary and read
+// after it, and written again only two boundaries later.
 template <int MODE>
 __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistArgs P) {
   __shared__ float s_bv[kPersistThreads / 64];
   __shared__ int s_bi[kPersistThreads / 64];
   __shared__ __attribute__((aligned(16))) uint32_t s_stage[2][kStageWords];
+  __shared__ int s_fail[2];
   const int blk = blockIdx.x, nblk = gridDim.x;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   TagIO io;
   io.abort_flag = P.abort_flag;
+  io.poll_limit = P.poll_limit;
+  if (t < 2) s_fail[t] = 0;   // first read after the first stage barrier
 
   // block-local copy of the generation state; every workgroup makes the same decisions
   int tok = P.ctl->tok, pos = P.ctl->pos, step = P.ctl->step, n_out = P.ctl->n_out;
@@ -51,7 +62,12 @@ __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistA
     io.tag0 = P.tag_base + (uint32_t)k * (uint32_t)kTagsPerToken;
     for (int i = 0; i < P.nstage; ++i) {
       if (t < kStageWords) s_stage[slot][t] = nxt;
+      if (io.failed) s_fail[slot] = 1;
       __syncthreads();
+      if (s_fail[slot] != 0) {   // workgroup-uniform: read after the barrier
+        aborted = 1;
+        break;
+      }
       const Stage& st = *reinterpret_cast<const Stage*>(s_stage[slot]);
       slot ^= 1;
       const int ni = i + 1 < P.nstage ? i + 1 : 0;   // the next stage (stage 0 after the head)
@@ -71,10 +87,7 @@ __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistA
         default: ok = head_body(st.hd, blk, nblk, io, P.logits); break;
       }
       if (tr != nullptr && t == 0) tr[kTraceSlots - 1] = __builtin_amdgcn_s_memrealtime();
-      if (!ok) {
-        aborted = 1;
-        break;
-      }
+      if (!ok) io.failed = true;   // the stage body refused its arguments: same exit
     }
     if (aborted) break;
     // argmax over the LM-head partials of all workgroups (qwen_synth.hpp:81-88), then ++pos (:90)
@@ -83,11 +96,9 @@ __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistA
     {
       float* pv = io.slot();
       float* pi = io.slot();
-      if (!io.stage_vec(hd.part_val, hd.part_st, nblk, pv) ||
-          !io.stage_vec(reinterpret_cast<const float*>(hd.part_idx), hd.part_st, nblk, pi)) {
-        aborted = 1;
-        break;
-      }
+      // (a failed wait here is noticed at the next stage boundary, or by the host)
+      io.stage_vec(hd.part_val, hd.part_st, nblk, pv);
+      io.stage_vec(reinterpret_cast<const float*>(hd.part_idx), hd.part_st, nblk, pi);
       for (int b = t; b < nblk; b += kPersistThreads) better(bv, bi, pv[b], __float_as_int(pi[b]));
     }
 #pragma unroll
@@ -105,7 +116,7 @@ __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistA
     bi = s_bi[0];
     for (int w2 = 1; w2 < kPersistThreads / 64; ++w2) better(bv, bi, s_bv[w2], s_bi[w2]);
     __syncthreads();
-    argmax = bi;
+    argmax = min(max(bi, 0), hd.rows - 1);   // a stale partial (after a failed wait) stays an index
     pos += 1;
     // run_hls.cpp:56-66: feed the prompt, then each greedy argmax until n_new or eos
     const int next = step + 1;

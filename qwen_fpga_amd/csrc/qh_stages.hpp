@@ -246,10 +246,20 @@ struct PlainIO {
 // roughly a microsecond): about a second, then the launch aborts.
 constexpr unsigned kPollLimit = 1u << 20;
 
+// Giving up: a wave whose wait reaches the poll limit (or that sees the abort
+// flag another wave set) marks itself failed and FINISHES the wait with the
+// stale values it holds, so it still passes every workgroup barrier of the
+// stage and takes part in the next stage's descriptor copy.  The persistent
+// kernel ORs the failure of all waves of a workgroup through LDS at the next
+// stage boundary, and the whole workgroup leaves together.  Stale values can
+// reach other workgroups as data but never as an address (the token fed back
+// is clamped to the vocabulary); those workgroups give up at their next miss.
 struct TagIO {
   static constexpr bool kTagged = true;
   uint32_t tag0 = 0;          // tag of stage 0 of the current token
   int* abort_flag = nullptr;  // global: set by the first wave that gives up
+  unsigned poll_limit = kPollLimit;
+  bool failed = false;        // this wave gave up a wait (sticky for the launch)
   int ring = 0;               // next LDS slot
   __device__ __forceinline__ float* slot() { return lds_ring() + kLdsSlot * (ring++ & 3); }
   uint64_t* tr = nullptr;     // optional timing trace of the current stage (points 0..2)
@@ -259,15 +269,19 @@ struct TagIO {
   __device__ __forceinline__ uint32_t tag(int st) const { return tag0 + (uint32_t)st; }
   __device__ __forceinline__ void arrive() {}
   __device__ __forceinline__ bool wait() { return true; }
-  // After a failed poll: false once the limit is reached or another wave gave up.
+  // After a failed poll: false (and the wave marked failed) once the limit is
+  // reached or another wave gave up.  A failed wave polls no more.
   __device__ __forceinline__ bool again(unsigned& polls) {
     ++polls;
-    if ((polls & 63u) == 0) {
-      if (polls > kPollLimit) {
-        stc_i(abort_flag, 1);
-        return false;
-      }
-      if (ldc_i(abort_flag) != 0) return false;
+    if (failed) return false;
+    if (polls > poll_limit) {
+      stc_i(abort_flag, 1);
+      failed = true;
+      return false;
+    }
+    if ((polls & 63u) == 0 && ldc_i(abort_flag) != 0) {
+      failed = true;
+      return false;
     }
     return true;
   }
@@ -310,7 +324,7 @@ struct TagIO {
     if (!tags16<N>(u, tg)) {
       unsigned polls = 0;
       do {   // after a miss, wait on one pair per lane before loading everything again
-        if (!again(polls) || !sample(rs, idx[N - 1] + 15, tg, polls)) return false;
+        if (!again(polls) || !sample(rs, idx[N - 1] + 15, tg, polls)) break;   // gave up: stale values
         issue16<N>(rs, idx, u);
       } while (!tags16<N>(u, tg));
     }
@@ -343,8 +357,8 @@ struct TagIO {
     if (!tags()) {
       unsigned polls = 0;
       do {
-        if (!again(polls)) return false;
-        if (N > 1 && !sample(rs, idx[N - 1], tg, polls)) return false;
+        if (!again(polls)) break;   // gave up: stale values
+        if (N > 1 && !sample(rs, idx[N - 1], tg, polls)) break;
         issue();
       } while (!tags());
     }
@@ -421,7 +435,7 @@ struct TagIO {
       const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
       unsigned polls = 0;
       do {
-        if (!again(polls) || !sample(rs, idx1[M - 1], tg, polls)) return false;
+        if (!again(polls) || !sample(rs, idx1[M - 1], tg, polls)) break;   // gave up: stale values
         poll_issue<N, M>(base, idx, idx1, P);
       } while (!tags());
       mark(4);   // trace: complete after a repoll
@@ -477,7 +491,7 @@ struct TagIO {
       const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
       unsigned polls = 0;
       do {
-        if (!again(polls) || !sample(rs, idx1[M - 1], tg, polls)) return false;
+        if (!again(polls) || !sample(rs, idx1[M - 1], tg, polls)) break;   // gave up: stale values
         pollr_issue<R, M>(base, rb, idx1, P);
       } while (!tags());
       mark(4);   // trace: complete after a repoll
@@ -568,7 +582,7 @@ struct TagIO {
       const unsigned sidx = (((unsigned)(lane >> 2) * k2) / 16u + 7u * (unsigned)blockIdx.x) % k2;
       unsigned polls = 0;
       do {
-        if (!again(polls) || !sample(rs, (int)(2 * sidx + 1), tg, polls)) return false;
+        if (!again(polls) || !sample(rs, (int)(2 * sidx + 1), tg, polls)) break;   // gave up: stale values
         stage_issue(base, K, vp);
       } while (!vec_tags(vp, K, tg));
       mark(4);   // trace: vector complete after a repoll

@@ -231,7 +231,8 @@ def pack(snapshot: str, out: str, idx_path: Optional[str] = None, check: bool = 
     missing = [k for k in order if k not in tensors]
     extra = [k for k in tensors if k not in order]
     if missing or extra:   # pack_weights.py:59-62
-        raise SystemExit(f"manifest/weights mismatch\n  missing: {missing[:5]}\n  extra: {extra[:5]}")
+        raise SystemExit(f"the snapshot's tensors do not match the packing order: {len(missing)} absent "
+                         f"(first {missing[:5]}), {len(extra)} not packed (first {extra[:5]})")
     entries, total = plan(order, {k: tensors[k].shape for k in order})
     idx = idx_text(entries)
     if idx != q.idx_text():
@@ -262,17 +263,13 @@ def pack(snapshot: str, out: str, idx_path: Optional[str] = None, check: bool = 
     with open(idx_path, "w") as f:
         f.write(idx)
     if verbose:
-        q_b = sum(e["nbytes"] for e in entries if e["dtype"] == "int8")
-        s_b = sum(e.get("scale_nbytes", 0) for e in entries)
-        f_b = sum(e["nbytes"] for e in entries if e["dtype"] == "fp32")
-        print(f"wrote {out}")
-        print(f"  int8 payload {q_b / 1e6:8.1f} MB")
-        print(f"  fp32 scales  {s_b / 1e6:8.2f} MB")
-        print(f"  fp32 tensors {f_b / 1e6:8.2f} MB")
-        print(f"  padding      {(total - q_b - s_b - f_b) / 1e6:8.2f} MB")
-        print(f"  TOTAL        {total / 1e6:8.1f} MB   ({total / 2 ** 20:.0f} MiB)")
-        print(f"wrote {mpath}")
-        print(f"wrote {idx_path}: {len(entries)} tensors")
+        parts = {"int8 weights": sum(e["nbytes"] for e in entries if e["dtype"] == "int8"),
+                 "row scales": sum(e.get("scale_nbytes", 0) for e in entries),
+                 "fp32 tensors": sum(e["nbytes"] for e in entries if e["dtype"] == "fp32")}
+        parts["alignment"] = total - sum(parts.values())
+        print(f"{out}: {total:,} bytes in {len(entries)} tensors ("
+              + ", ".join(f"{k} {v:,}" for k, v in parts.items()) + ")")
+        print(f"{mpath}: manifest; {idx_path}: weight index")
     if check:
         worst = check_blob(out, entries, tensors)
         if verbose:

@@ -7,7 +7,10 @@
   compiled hls/src kernels): identical argmax at every one of 576 steps;
 * the run_hls generation loop (hls/tb/run_hls.cpp:56-66) on the device against
   a host loop of decode_token calls, eos handling, context limits, reset;
-* layers [0, 4) as one block (C4), and the qh_run_hls CLI.
+* the benchmarked configuration (persistent executor, W8A8, 64 + 512 tokens in
+  one launch) bit for bit against the twin; the argmax tie rule across
+  workgroups; a forced hand-over give-up that every wave survives;
+* layers [0, 4) as one block for 128 steps (C4), and the qh_run_hls CLI.
 """
 import ctypes
 import json
@@ -73,7 +76,7 @@ def test_decode_matches_device_twin(q, orc, engine, model, mode):
 
 @pytest.mark.parametrize("mode", [0, 1], ids=["w8a16", "w8a8"])
 def test_persistent_equals_graph_path(q, engine, mode):
-    """The persistent kernel (one launch, grid barriers) and the per-stage graph give the same bits."""
+    """The persistent kernel (one launch, tagged hand-overs) and the per-stage graph give the same bits."""
     default = engine.exec_kind
     engine.set_mode(mode)
     toks = [5, 248319, 17, 0, 99999, 3]
@@ -155,29 +158,148 @@ def test_context_limit(q, blob, torch_cuda):
         e.close()
 
 
-def test_forward_layers_block(orc, engine, model, torch_cuda):
-    """C4: layers [0, 4) = 3 DeltaNet + 1 attention on a random hidden vector, twice."""
+@pytest.mark.parametrize("mode", [0, 1], ids=["w8a16", "w8a8"])
+def test_forward_layers_block_c4(q, orc, blob, idx, torch_cuda, mode):
+    """C4: layers [0, 4) = 3 DeltaNet + 1 attention, 128 decode steps, each on a fresh hidden
+    vector ~ N(0, 1) (the states and the KV cache evolve); every output and the final states
+    bit for bit against the device twin."""
     torch = torch_cuda
-    engine.set_mode(0)
-    engine.reset()
-    model.reset()
-    r = rng(404)
-    for step in range(3):
-        h = np.ascontiguousarray(r.standard_normal(1024), dtype=np.float32)
-        hd = torch.from_numpy(h.copy()).cuda()
-        engine.forward_layers(0, 4, hd)
-        ho = h.copy()
-        model.forward_layers(0, 4, ho, mode=orc.W8A16, order=orc.ORDER_DEV)
-        assert_bitwise(hd.cpu().numpy(), ho, f"block output step {step}")
-    assert engine.pos == 3
+    n = 128
+    e = q.Engine(blob, max_ctx=n, mode=mode)
+    m = orc.Model(blob, idx, max_ctx=n)
+    try:
+        r = rng(404 + mode)
+        for step in range(n):
+            h = np.ascontiguousarray(r.standard_normal(1024), dtype=np.float32)
+            hd = torch.from_numpy(h.copy()).cuda()
+            e.forward_layers(0, 4, hd)
+            ho = h.copy()
+            m.forward_layers(0, 4, ho, mode=mode, order=orc.ORDER_DEV)
+            assert_bitwise(hd.cpu().numpy(), ho, f"block output step {step}")
+        assert e.pos == m.pos == n
+        assert_bitwise(d2h(e.device_ptr(1), (18, 16, 128, 128))[:3], m.rec()[:3], "recurrent state")
+        assert_bitwise(d2h(e.device_ptr(2), (18, 6144, 4))[:3], m.conv()[:3], "conv state")
+        assert_bitwise(d2h(e.device_ptr(3), (6, n, 512))[0], m.kcache()[0], "k cache")
+        assert_bitwise(d2h(e.device_ptr(4), (6, n, 512))[0], m.vcache()[0], "v cache")
+    finally:
+        e.close()
+        m.close()
+
+
+def test_persistent_full_c5_w8a8_vs_twin(q, orc, blob, idx, torch_cuda):
+    """The benchmarked path at the benchmarked length: the persistent executor, W8A8, the C5
+    prompt (64 seeded ids) and 512 greedy tokens in ONE launch (KV to 576, the multi-chunk
+    combine past 512 positions), against the device twin: every generated id and, at the end,
+    every recurrent / conv / KV buffer bit for bit; then the same stream token by token with
+    the logits of chosen steps bit for bit."""
+    npr, nn = 64, 512
+    prompt = rng(1234).integers(0, q.VOCAB, size=npr).astype(np.int32).tolist()
+    n = npr + nn
+    keep = {0, 63, 64, 300, 511, 574}
+    m = orc.Model(blob, idx, max_ctx=n)
+    fed, twin_am, twin_lg = [], [], {}
+    cur = None
+    for i in range(n):   # the run_hls loop: prompt, then each argmax fed back (n passes in all)
+        tok = prompt[i] if i < npr else cur
+        cur, lg = m.decode_token(tok, mode=orc.W8A8, order=orc.ORDER_DEV, want_logits=i in keep)
+        fed.append(tok)
+        twin_am.append(cur)
+        if i in keep:
+            twin_lg[i] = lg
+    e = q.Engine(blob, max_ctx=n, mode=q.MODE_W8A8)
+    try:
+        e.set_exec(q.EXEC_PERSISTENT)
+        gen = e.generate(prompt, nn)
+        assert e.exec_kind == q.EXEC_PERSISTENT, "the cooperative launch was refused"
+        assert gen == twin_am[npr - 1:n - 1]
+        assert e.pos == m.pos == n
+        assert_bitwise(d2h(e.device_ptr(1), (18, 16, 128, 128)), m.rec(), "recurrent state")
+        assert_bitwise(d2h(e.device_ptr(2), (18, 6144, 4)), m.conv(), "conv state")
+        assert_bitwise(d2h(e.device_ptr(3), (6, n, 512)), m.kcache(), "k cache")
+        assert_bitwise(d2h(e.device_ptr(4), (6, n, 512)), m.vcache(), "v cache")
+        e.reset()
+        for i, tok in enumerate(fed):
+            am, lg = e.decode_token(tok, want_logits=i in keep)
+            assert am == twin_am[i], f"step {i}: {am} vs twin {twin_am[i]}"
+            if i in keep:
+                assert_bitwise(lg, twin_lg[i], f"logits step {i}")
+    finally:
+        e.close()
+        m.close()
+
+
+@pytest.mark.parametrize("exec_kind", ["graph", "persistent"])
+def test_argmax_tie_lowest_index_wins(q, orc, blob, idx, torch_cuda, exec_kind):
+    """qwen_synth.hpp:81-88 / decoder.hpp:115: strict > from -1e30, so of equal logits the lowest
+    index wins.  Row a (the argmax) of the tied embedding is copied to a lower row in another
+    workgroup's range (that row must now win) and, separately, to a higher one (a must stay)."""
+    tok = 17
+    e0 = q.Engine(blob, max_ctx=4)
+    a, _ = e0.decode_token(tok)
+    e0.close()
+    emb = q.parse_idx(idx)["embed_tokens.weight"]
+    stride = 256 * 4   # head batches of 8 rows, one per wave, over 256 workgroups of 4 waves
+
+    def blk_of(r):
+        return ((r // 8) % stride) // 4
+
+    low = next(r for r in range(a // 3, a) if blk_of(r) != blk_of(a) and r != tok)
+    high = next(r for r in range(a + (q.VOCAB - a) // 2, q.VOCAB) if blk_of(r) != blk_of(a) and r != tok)
+    for other, want in ((low, low), (high, a)):
+        b = blob.copy()
+        row = slice(emb.off + a * 1024, emb.off + (a + 1) * 1024)
+        b[emb.off + other * 1024:emb.off + (other + 1) * 1024] = b[row]
+        b[emb.soff + 4 * other:emb.soff + 4 * other + 4] = b[emb.soff + 4 * a:emb.soff + 4 * a + 4]
+        m = orc.Model(b, idx, max_ctx=4)
+        am_t, lg_t = m.decode_token(tok, mode=orc.W8A16, order=orc.ORDER_DEV, want_logits=True)
+        m.close()
+        assert lg_t[other] == lg_t[a] and am_t == want
+        e = q.Engine(b, max_ctx=4)
+        try:
+            e.set_exec(q.EXEC_GRAPH if exec_kind == "graph" else q.EXEC_PERSISTENT)
+            am, lg = e.decode_token(tok, want_logits=True)
+            assert lg[other] == lg[a], "tied rows must give identical logits"
+            assert am == want, f"tie between {a} and {other}: argmax {am}, want {want}"
+        finally:
+            e.close()
+
+
+def test_abort_exits_every_wave(q, blob, torch_cuda, monkeypatch):
+    """A hand-over wait that gives up (forced from the host: QH_POLL_LIMIT=0 makes the first miss
+    final) ends the launch with every workgroup leaving together: the call returns QH_EDEVICE,
+    the engine refuses to decode until reset, and after the reset it decodes like a fresh one."""
+    monkeypatch.setenv("QH_POLL_LIMIT", "0")
+    e = q.Engine(blob, max_ctx=64)
+    monkeypatch.delenv("QH_POLL_LIMIT")
+    f = q.Engine(blob, max_ctx=64)
+    try:
+        e.set_exec(q.EXEC_PERSISTENT)
+        with pytest.raises(q.QHError) as ex:
+            e.generate([11, 2222, 33333, 44], 16)
+        assert ex.value.status == q.QH_EDEVICE
+        with pytest.raises(q.QHError) as ex:
+            e.decode_token(5)
+        assert ex.value.status == q.QH_ESTATE
+        e.reset()
+        e.set_exec(q.EXEC_GRAPH)   # the graph path has no hand-over waits
+        f.set_exec(q.EXEC_GRAPH)
+        a1, l1 = e.decode_token(5, want_logits=True)
+        a2, l2 = f.decode_token(5, want_logits=True)
+        assert a1 == a2
+        assert_bitwise(l1, l2, "after reset")
+    finally:
+        e.close()
+        f.close()
 
 
 GOLD = os.path.join(GOLDEN, "decode_ref_c5.json")
 
 
 @pytest.mark.skipif(not os.path.exists(GOLD), reason="golden decode fixture not generated")
-def test_reference_argmax_stream_c5(q, blob):
-    """C5: 64-token prompt + 512 greedy tokens; argmax identical to the reference at every step."""
+@pytest.mark.parametrize("exec_kind", ["graph", "persistent"])
+def test_reference_argmax_stream_c5(q, blob, exec_kind):
+    """C5: 64-token prompt + 512 greedy tokens; argmax identical to the reference at every step,
+    token by token and as one generate call, on both executors."""
     import hashlib
 
     g = json.load(open(GOLD))
@@ -185,6 +307,7 @@ def test_reference_argmax_stream_c5(q, blob):
     n = len(g["fed"])
     e = q.Engine(blob, max_ctx=n)
     try:
+        e.set_exec(q.EXEC_GRAPH if exec_kind == "graph" else q.EXEC_PERSISTENT)
         for i, tok in enumerate(g["fed"]):
             want = str(i) in g["logits"]
             am, lg = e.decode_token(tok, want_logits=want)
@@ -198,6 +321,7 @@ def test_reference_argmax_stream_c5(q, blob):
         npr = g["n_prompt"]
         gen = e.generate(g["fed"][:npr], g["n_new"])
         assert gen == g["argmax"][npr - 1:npr - 1 + g["n_new"]]
+        assert e.exec_kind == (q.EXEC_GRAPH if exec_kind == "graph" else q.EXEC_PERSISTENT)
     finally:
         e.close()
 
