@@ -141,6 +141,18 @@ int qh_attention_layer(float* out, const float* x, const qh_tensor* q_w, const q
 /* SwiGLU MLP: down(silu(gate x) * up x)                      mlp.hpp:11-19 mlp_layer */
 int qh_mlp_layer(float* out, const float* x, const qh_tensor* gate_w, const qh_tensor* up_w,
                  const qh_tensor* down_w, void* stream);
+/* qh_attention_layer (mode QH_MODE_W8A16) or qh_attention_layer_w8a8 (QH_MODE_W8A8) without any
+ * allocation: no counterpart in the reference; for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, kernels and results; the intermediate vectors live in one file-scope device array
+ * of the library (4.3 MB on every GPU the library runs on, held until the process ends), so
+ * T + 1 <= 8192 -- the reference's own sc[8192] bound (attention.hpp:66) -- else QH_ERANGE.
+ * Every call on one GPU uses that GPU's array: calls that overlap on one GPU (other streams,
+ * other host threads) race and must be serialised by the caller. */
+int qh_attention_layer_noalloc(float* out, const float* x, const qh_tensor* q_w, const qh_tensor* k_w,
+                               const qh_tensor* v_w, const qh_tensor* o_w, const float* q_norm,
+                               const float* k_norm, int pos, float* kcache, float* vcache, int T, int mode,
+                               void* stream);
 
 /* ---- W8A8 (int8 activation) entry points; no C++ counterpart in hls/src ----
  * per-vector symmetric int8: s = amax/127 (1 if amax == 0), q = rint(x/s) clipped to +-127.

@@ -285,6 +285,16 @@ def attention_layer(out, x, q_w: Tensor, k_w: Tensor, v_w: Tensor, o_w: Tensor, 
           _dev(vcache, "f32", n_kv, "vcache"), T, _Ptr(_stream(stream)))
 
 
+def attention_layer_noalloc(out, x, q_w: Tensor, k_w: Tensor, v_w: Tensor, o_w: Tensor, q_norm, k_norm, pos: int,
+                            kcache, vcache, T: int, w8a8: bool = False, stream=None):
+    """attention_layer without any device allocation (the library's static scratch; T + 1 <= 8192)."""
+    n_kv = (max(T, 0) + 1) * 512
+    _call("qh_attention_layer_noalloc", _dev(out, "f32", HIDDEN, "out"), _dev(x, "f32", HIDDEN, "x"), q_w, k_w,
+          v_w, o_w, _dev(q_norm, "f32", 256, "q_norm"), _dev(k_norm, "f32", 256, "k_norm"), pos,
+          _dev(kcache, "f32", n_kv, "kcache"), _dev(vcache, "f32", n_kv, "vcache"), T,
+          MODE_W8A8 if w8a8 else MODE_W8A16, _Ptr(_stream(stream)))
+
+
 def mlp_layer(out, x, gate_w: Tensor, up_w: Tensor, down_w: Tensor, w8a8: bool = False, stream=None):
     _call("qh_mlp_layer_w8a8" if w8a8 else "qh_mlp_layer", _dev(out, "f32", HIDDEN, "out"),
           _dev(x, "f32", HIDDEN, "x"), gate_w, up_w, down_w, _Ptr(_stream(stream)))

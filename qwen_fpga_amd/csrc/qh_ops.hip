@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 #include "qh_common.hpp"
 #include "qh_kernels.hpp"
@@ -41,14 +42,20 @@ namespace {
 
 hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-// Stream-ordered scratch: one allocation carved into 256-byte aligned pieces.
+// Scratch carved into 256-byte aligned pieces: one stream-ordered allocation
+// (hipMallocAsync / hipFreeAsync on the caller's stream), or -- for the
+// entry point that allocates nothing -- a caller-provided device buffer.
 struct Scratch {
   hipStream_t s;
   char* base = nullptr;
   size_t size = 0, used = 0;
-  explicit Scratch(hipStream_t st) : s(st) {}
+  bool owned = false;
+  explicit Scratch(hipStream_t st, char* given = nullptr, size_t given_size = 0)
+      : s(st), base(given), size(given_size) {}
   int alloc(size_t total) {
+    if (base != nullptr) return total <= size ? QH_OK : QH_ERANGE;   // given buffer: just check the fit
     size = total;
+    owned = true;
     return hip_status(hipMallocAsync(reinterpret_cast<void**>(&base), total, s));
   }
   template <class T>
@@ -59,10 +66,47 @@ struct Scratch {
     return p;
   }
   ~Scratch() {
-    if (base) (void)hipFreeAsync(base, s);
+    if (owned && base) (void)hipFreeAsync(base, s);
   }
 };
-size_t rnd(size_t bytes) { return (bytes + 255) & ~(size_t)255; }
+constexpr size_t rnd(size_t bytes) { return (bytes + 255) & ~(size_t)255; }
+
+// Scratch of one attention_layer call with ns splits: q||gate|k|v, the RoPE row, T and
+// the RoPE row index, split maxima / sums / partial contexts, the gated context.
+constexpr size_t attention_scratch_bytes(int ns) {
+  return rnd(4 * (kQProj + 2 * kKVProj)) + rnd(4 * 64) + rnd(8) + 2 * rnd(4 * 8 * (size_t)ns) +
+         rnd(4 * 8 * 256 * (size_t)ns) + rnd(4 * kNH * kHD);
+}
+
+// ---- the scratch of qh_attention_layer_noalloc: one file-scope device array ----
+// Contexts up to the reference's own bound, sc[8192] (attention.hpp:66): T + 1 <= 8192,
+// 512 splits of 16 positions: 4.3 MB held on every GPU the library runs on until the
+// process ends.  In host code `scratch` names a host-side stand-in, not the device
+// array: its device address is taken once per device (hipGetSymbolAddress, with that
+// device current) and only that address reaches kernels.
+constexpr int kNoallocMaxCtx = 8192;
+constexpr size_t kNoallocBytes = attention_scratch_bytes(kNoallocMaxCtx / kAttnSplit);
+static_assert(kNoallocMaxCtx % kAttnSplit == 0 && kNoallocBytes < (size_t)5 << 20, "a modest, fixed maximum");
+__device__ __align__(256) char scratch[kNoallocBytes];
+constexpr int kMaxDevices = 64;
+char* g_scratch_dev[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+// The device address of `scratch` on the current device, looked up on the first call there.
+int noalloc_scratch(char** out) {
+  int dev = 0;
+  QH_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return QH_EINVAL;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* ptr = nullptr;
+    QH_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (ptr == nullptr) return QH_ENOMEM;
+    g_scratch_dev[dev] = static_cast<char*>(ptr);
+  }
+  *out = g_scratch_dev[dev];
+  return QH_OK;
+}
 
 bool tensor_i8(const qh_tensor* t, int out, int in) {
   return t && t->w_i8 && t->scale && t->out == out && t->in == in && aligned16(t->w_i8);
@@ -145,9 +189,11 @@ int deltanet_layer(float* out, const float* x, const qh_tensor* qkv_w, const qh_
   return QH_OK;
 }
 
+// given: a device buffer of given_size bytes to carve the scratch from (no allocation), or null
 int attention_layer(float* out, const float* x, const qh_tensor* q_w, const qh_tensor* k_w,
                     const qh_tensor* v_w, const qh_tensor* o_w, const float* q_norm, const float* k_norm,
-                    int pos, float* kcache, float* vcache, int T, int mode, hipStream_t s) {
+                    int pos, float* kcache, float* vcache, int T, int mode, hipStream_t s,
+                    char* given = nullptr, size_t given_size = 0) {
   if (!out || !x || !q_norm || !k_norm || !kcache || !vcache) return QH_EINVAL;
   if (T < 0 || pos < 0 || T >= QH_MAX_CTX) return QH_ERANGE;
   if (!tensor_i8(q_w, kQProj, kHidden) || !tensor_i8(k_w, kKVProj, kHidden) ||
@@ -157,9 +203,8 @@ int attention_layer(float* out, const float* x, const qh_tensor* q_w, const qh_t
     return QH_EINVAL;
   const int Tn = T + 1;
   const int ns = (Tn + kAttnSplit - 1) / kAttnSplit;
-  Scratch sc(s);
-  QH_TRY(sc.alloc(rnd(4 * (kQProj + 2 * kKVProj)) + rnd(4 * 64) + rnd(8) + 2 * rnd(4 * 8 * (size_t)ns) +
-                  rnd(4 * 8 * 256 * (size_t)ns) + rnd(4 * kNH * kHD)));
+  Scratch sc(s, given, given_size);
+  QH_TRY(sc.alloc(attention_scratch_bytes(ns)));
   float* qkv = sc.take<float>(kQProj + 2 * kKVProj);   // q||gate | k | v
   float* qg = qkv;
   float* kraw = qkv + kQProj;
@@ -436,6 +481,20 @@ int qh_attention_layer_w8a8(float* out, const float* x, const qh_tensor* q_w, co
                             const float* k_norm, int pos, float* kcache, float* vcache, int T, void* stream) {
   return attention_layer(out, x, q_w, k_w, v_w, o_w, q_norm, k_norm, pos, kcache, vcache, T, M_W8A8,
                          S(stream));
+}
+
+int qh_attention_layer_noalloc(float* out, const float* x, const qh_tensor* q_w, const qh_tensor* k_w,
+                               const qh_tensor* v_w, const qh_tensor* o_w, const float* q_norm,
+                               const float* k_norm, int pos, float* kcache, float* vcache, int T, int mode,
+                               void* stream) {
+  if (mode != QH_MODE_W8A16 && mode != QH_MODE_W8A8) return QH_EINVAL;
+  if (T < 0 || T + 1 > kNoallocMaxCtx) return QH_ERANGE;
+  char* base = nullptr;
+  QH_TRY(noalloc_scratch(&base));
+  const int ns = (T + 1 + kAttnSplit - 1) / kAttnSplit;
+  if (attention_scratch_bytes(ns) > kNoallocBytes) return QH_ERANGE;
+  return attention_layer(out, x, q_w, k_w, v_w, o_w, q_norm, k_norm, pos, kcache, vcache, T,
+                         mode == QH_MODE_W8A8 ? M_W8A8 : M_W8A16, S(stream), base, kNoallocBytes);
 }
 
 int qh_mlp_layer(float* out, const float* x, const qh_tensor* gate_w, const qh_tensor* up_w,
