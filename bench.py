@@ -64,6 +64,7 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--cpu-tokens", type=int, default=8, help="reference CPU decode sample (tokens)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the per-config C1-C4 op measurements")
     ap.add_argument("--profile-steps", type=int, default=16)
     ap.add_argument("--exec", dest="exec_kind", choices=["graph", "persistent"], default="persistent",
                     help="persistent: one cooperative launch runs every token, stages hand vectors over "
@@ -181,42 +182,185 @@ def main() -> int:
         "frac_of_roofline": round(achieved_gbs / PEAK_GBS, 4),
         "roofline": roofline,
     }
+    # the other activation mode on the same executor and workload (reported beside `value`)
+    other = q.MODE_W8A16 if mode == q.MODE_W8A8 else q.MODE_W8A8
+    eng.set_mode(other)
+    eng.reset()
+    eng.generate(prompt, 0)
+    cur = eng.last_argmax
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    eng.generate([cur], args.steps - 1)
+    torch.cuda.synchronize()
+    line["value_" + ("w8a16" if other == q.MODE_W8A16 else "w8a8")] = round(args.steps / (time.perf_counter() - t0), 2)
     eng.close()
 
+    if not args.no_configs:
+        line["configs"] = op_configs(q, torch, np, blob, idx, args.mode)
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(blob, idx, prompt, args.cpu_tokens)
+        line["cpu_baseline"] = cpu_baseline(blob, idx, prompt, args.cpu_tokens, args.mode)
     print(json.dumps(line), flush=True)
     return 0
 
 
-def cpu_baseline(blob, idx, prompt, ntok):
-    """The reference decode top on the host: the compiled hls/src qwen_top when
-    oracle/_ref is built, else the C restatement in reference order; one core."""
-    import oracle
+def _timed(torch, fn, iters):
+    """Median microseconds of one fn(i) call, from a pair of HIP events recorded right before
+    and after it on the stream it runs on (the host enqueues slower than these kernels run,
+    so timing a whole loop would time the host)."""
+    s = torch.cuda.current_stream()
+    fn()
+    s.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    for i, (a, b) in enumerate(ev):
+        a.record(s)
+        fn(i)
+        b.record(s)
+    s.synchronize()
+    t = sorted(a.elapsed_time(b) * 1e3 for a, b in ev)
+    return t[len(t) // 2]
 
-    toks = prompt[:ntok]
+
+def _rate(bytes_per_unit, us):
+    gbs = bytes_per_unit / (us * 1e-6) / 1e9
+    return {"us": round(us, 2), "bytes": int(bytes_per_unit), "gbs": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
+
+
+def op_configs(q, torch, np, blob, idx, act_mode):
+    """BASELINE.json configs C1-C4 on the op-level C ABI (the standalone kernels of the
+    graph executor), each unit timed with HIP events on the stream it runs on; bytes per
+    unit are the algorithmic counts of the configs (weights + scales + activations + state
+    / cache traffic).  C1 rotates through > 256 MB of weight copies so that no call is
+    served by the 256 MB Infinity Cache."""
+    dev = torch.device("cuda")
+    w8a8 = act_mode == "w8a8"
+    rng = np.random.default_rng(7)
+    out = {}
+
+    # C1: int8 GEMV, W int8 U{-127..127}, scales U[1e-3,1e-2], x ~ N(0,1) quantised per tensor
+    c1 = []
+    for n, k in ((3584, 1024), (1024, 3584), (6144, 1024)):
+        copies = -(-300_000_000 // (n * k))
+        W = torch.from_numpy(q.synth_i8(copies * n * k, 11 + n)).to(dev).view(copies, n, k)
+        sw = torch.from_numpy(q.synth_uniform(copies * n, 13 + n, 1e-3, 1e-2)).to(dev).view(copies, n)
+        x = torch.from_numpy(rng.standard_normal(k).astype(np.float32)).to(dev)
+        xq = torch.empty(k, dtype=torch.int8, device=dev)
+        sx = torch.empty(1, device=dev)
+        y = torch.empty(n, device=dev)
+        q.quant_act(xq, sx, x, k)
+        if w8a8:
+            us = _timed(torch, lambda i=0: q.gemv_i8_w8a8(y, None, W[i % copies], sw[i % copies], xq, sx, n, k), 200)
+            nbytes = n * k + 4 * n + k + 4 + 4 * n
+        else:
+            us = _timed(torch, lambda i=0: q.gemv_i8(y, W[i % copies], sw[i % copies], x, n, k), 200)
+            nbytes = n * k + 4 * n + 4 * k + 4 * n
+        c1.append(dict(shape=f"{n}x{k}", **_rate(nbytes, us)))
+        del W, sw
+    out["C1_gemv"] = c1
+
+    # C2: the recurrent delta-rule step of 16 heads on a warm fp32 state S0 ~ N(0, 0.05),
+    # q, k l2-normalised, beta = sigmoid(N(0,1)), g = -softplus(N(0,1)) * A, A ~ U[1,16]; 64 steps
+    S = torch.from_numpy((0.05 * rng.standard_normal((16, 128, 128))).astype(np.float32)).to(dev)
+    qkv = rng.standard_normal((3, 16, 128)).astype(np.float32)
+    qkv[:2] /= np.linalg.norm(qkv[:2], axis=-1, keepdims=True)
+    qd, kd, vd = (torch.from_numpy(np.ascontiguousarray(a)).to(dev) for a in qkv)
+    beta = torch.from_numpy((1 / (1 + np.exp(-rng.standard_normal(16)))).astype(np.float32)).to(dev)
+    g = torch.from_numpy((-np.log1p(np.exp(rng.standard_normal(16))) * rng.uniform(1, 16, 16)).astype(np.float32)).to(dev)
+    o = torch.empty(16 * 128, device=dev)
+    us = _timed(torch, lambda i=0: q.delta_rule_layer(qd, kd, vd, g, beta, S, o), 64)
+    out["C2_delta_rule_step"] = dict(steps=64, **_rate(2 * 16 * 128 * 128 * 4 + 4 * 3 * 2048 + 4 * 32 + 4 * 2048, us))
+
+    # C3: the gated GQA attention layer (projections, QK-norm, RoPE, split-K softmax, gate, o_proj)
+    # over an fp32 N(0,1) KV cache of T past tokens
+    e = q.parse_idx(idx)
+    p = "layers.3.self_attn."
+
+    def up_i8(name):
+        t = e[name]
+        wq = blob[t.off:t.off + t.nbytes].view(np.int8).reshape(t.out, t.in_)
+        return q.Tensor.i8(torch.from_numpy(wq.copy()).to(dev),
+                           torch.from_numpy(blob[t.soff:t.soff + t.snbytes].view(np.float32).copy()).to(dev))
+
+    def up_f32(name):
+        t = e[name]
+        return torch.from_numpy(blob[t.off:t.off + t.nbytes].view(np.float32).copy()).to(dev)
+
+    keep = [up_i8(p + n + "_proj.weight") for n in ("q", "k", "v", "o")]
+    qn, kn = up_f32(p + "q_norm.weight"), up_f32(p + "k_norm.weight")
+    xa = torch.from_numpy(rng.standard_normal(1024).astype(np.float32)).to(dev)
+    ya = torch.empty(1024, device=dev)
+    c3 = []
+    for T in (512, 4096, 32768):
+        kc = torch.randn((T + 1) * 512, device=dev)
+        vc = torch.randn((T + 1) * 512, device=dev)
+        us = _timed(torch, lambda i=0: q.attention_layer(ya, xa, *keep, qn, kn, T, kc, vc, T, w8a8=w8a8), 50)
+        c3.append(dict(T=T, **_rate(7_364_608 + 2_048 + 4_096 * T + 4_096, us)))
+        del kc, vc
+    out["C3_attention"] = c3
+
+    # C4: layers 0-3 (3 DeltaNet + 1 attention, each with its MLP) as the engine's per-stage
+    # kernels, 128 decode steps on fresh hidden vectors ~ N(0,1)
+    eng = q.Engine(blob, idx=idx, max_ctx=130, mode=q.MODE_W8A8 if w8a8 else q.MODE_W8A16)
+    h = torch.from_numpy(rng.standard_normal(1024).astype(np.float32)).to(dev)
+    eng.forward_layers(0, 4, h)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(128):
+        eng.forward_layers(0, 4, h)
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) * 1e6 / 128
+    eng.close()
+    out["C4_block"] = dict(steps=128, note="host-timed per step (one synchronising call each)",
+                           **_rate(90_709_888 + 4_096 * 66, us))
+    return out
+
+
+def _blas_threads():
+    try:
+        from threadpoolctl import threadpool_info
+        n = [i.get("num_threads") for i in threadpool_info() if i.get("user_api") == "blas"]
+        return int(n[0]) if n else 1
+    except Exception:
+        return int(os.environ.get("OPENBLAS_NUM_THREADS", "1"))
+
+
+def cpu_baseline(blob, idx, prompt, ntok, act_mode):
+    """The reference's CPU paths on this host, same synthetic model and prompt.  Primary
+    (same activation mode as the GPU line): this repository's numpy restatement of the
+    reference golden decode (golden/model.py; oracle/numpy_golden.py, pinned to fixtures the
+    reference wrote), numpy's BLAS threads; the legs add the other mode and the reference's
+    own hls/src decode top compiled natively (W8A16 only, one core)."""
+    import oracle
+    import oracle.numpy_golden as ng
+    import qwen_fpga_amd as q
+
+    entries = q.parse_idx(idx)
+    legs = []
+    for mode in (act_mode, "w8a16" if act_mode == "w8a8" else "w8a8"):
+        g = ng.Golden(blob, entries, act_int8=mode == "w8a8")
+        g.decode_step(int(prompt[0]))   # first touch of the weights
+        g.reset()
+        n = 2 * ntok
+        t0 = time.perf_counter()
+        for t in prompt[:n]:
+            g.decode_step(int(t))
+        dt = time.perf_counter() - t0
+        legs.append({"value": round(n / dt, 3), "unit": "tok/s", "cores": _blas_threads(), "kind": "port",
+                     "sample": f"{n} decode tokens from a fresh state, numpy golden decode restated "
+                               f"(golden/model.py, {mode}; numpy BLAS threads, host nproc {os.cpu_count()})"})
+        del g
     if oracle.ref() is not None:
         m = oracle.RefModel(blob)
         t0 = time.perf_counter()
-        for t in toks:
+        for t in prompt[:ntok]:
             m.qwen_top(int(t))
         dt = time.perf_counter() - t0
-        kind, what = "reference", "reference hls/src qwen_top compiled -O2 -ffp-contract=off (csim build)"
-    else:
-        oracle.lib().or_set_threads(1)
-        m = oracle.Model(blob, idx, len(toks) + 1)
-        t0 = time.perf_counter()
-        for t in toks:
-            m.decode_token(int(t))
-        dt = time.perf_counter() - t0
-        kind, what = "port", "oracle.c reference-order restatement, single thread"
-    return {"value": round(len(toks) / dt, 4), "unit": "tok/s", "cores": 1, "kind": kind,
-            "sample": f"{len(toks)} decode tokens of the same synthetic model from a fresh state ({what})"}
+        legs.append({"value": round(ntok / dt, 4), "unit": "tok/s", "cores": 1, "kind": "reference",
+                     "sample": f"{ntok} decode tokens from a fresh state, the reference hls/src qwen_top compiled "
+                               f"-O2 -ffp-contract=off (csim build; w8a16)"})
+    out = dict(legs[0])
+    out["legs"] = legs[1:]
+    return out
 
 
 if __name__ == "__main__":
-    # a successful run ends normally: sys.exit(0) takes an exit path in which a
-    # profiler attached to the process (rocprofv3) fails before writing its records
-    rc = main()
-    if rc:
-        sys.exit(rc)
+    sys.exit(main())

@@ -292,3 +292,18 @@ def test_teacher_forced_stream(orc, blob, idx, mode):
         print(mode, chk.finish())
     finally:
         m.close()
+
+
+@pytest.mark.skipif(not os.path.exists(gn.stream_path("w8a8")), reason="golden stream not generated")
+@pytest.mark.parametrize("mode", ["w8a16", "w8a8"])
+def test_numpy_restatement_equals_golden(blob, entries, mode):
+    """oracle/numpy_golden.py (bench.py's CPU port of golden/model.py) reproduces the golden's
+    logits bit for bit on the first steps of its stream (same numpy operations, same order)."""
+    import oracle.numpy_golden as ng
+
+    g = gn.load_stream(mode)
+    m = ng.Golden(blob, entries, act_int8=mode == "w8a8")
+    for i in range(12):
+        lg = m.decode_step(g["fed"][i])
+        assert int(np.argmax(lg)) == g["argmax"][i], f"step {i}"
+        assert_bitwise(lg[g["top8_ids"][i]], np.array(g["top8_vals"][i], np.float32), f"top-8 logits step {i}")
