@@ -33,19 +33,23 @@ HEAD_BYTES = 248320 * 1024 + 248320 * 4 + 2 * 4096   # int8 rows + scales + h + 
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "head_kernel_decode_c5_pmc_traffic.md")
+PERSIST_TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "persist_kernel_decode_c5_pmc_traffic.md")
 
 
-def head_traffic():
-    """HBM bytes per head_kernel launch from the committed rocprofv3 counter
-    summary (FETCH_SIZE + WRITE_SIZE, each scaled by a copy of known size); the
-    counters cannot be read from inside this process."""
+def profile_value(path, key):
+    """A figure from a committed rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE, each
+    scaled by a copy of known size); the counters cannot be read from inside this process."""
     try:
-        for line in open(TRAFFIC_PROFILE):
-            if line.startswith("traffic_bytes_per_launch:"):
+        for line in open(path):
+            if line.startswith(key + ":"):
                 return int(line.split(":")[1])
     except OSError:
         pass
     return None
+
+
+def head_traffic():
+    return profile_value(TRAFFIC_PROFILE, "traffic_bytes_per_launch")
 
 
 def full_bytes(T: int) -> int:
@@ -124,14 +128,20 @@ def main() -> int:
         # launch duration from HIP events recorded around it on the engine stream
         launch_ms = eng.last_launch_ms
         launch_bytes = int(mean_full * args.steps)
+        per_tok = profile_value(PERSIST_TRAFFIC_PROFILE, "traffic_bytes_per_token")
         roofline = {
             "kernel": "persist_kernel (every stage of every token in one cooperative launch)",
+            # the only roofline of a ~2 op/B int8 GEMV datapath; the counters show ~1.05x the
+            # algorithmic bytes cross HBM, so the gap to it is latency (126 dependent all-to-all
+            # hand-overs per token), not traffic
             "bound": "hbm",
+            "limiter": "latency of the per-stage hand-overs and post-arrival chains (traffic 1.05x algorithmic)",
             "achieved": round(launch_bytes / (launch_ms * 1e-3) / 1e9, 1),
             "peak": PEAK_GBS,
             "unit": "GB/s",
             "frac": round(launch_bytes / (launch_ms * 1e-3) / 1e9 / PEAK_GBS, 4),
-            "traffic": None,   # rocprofv3 --pmc cannot complete on the cooperative kernel
+            # FETCH_SIZE + WRITE_SIZE per token of a 64-token launch (committed summary) x tokens
+            "traffic": per_tok * args.steps if per_tok else None,
             "duration_us": round(launch_ms * 1e3, 1),
             "bytes_per_launch": launch_bytes,
             "tokens_per_launch": args.steps,
@@ -363,4 +373,11 @@ def cpu_baseline(blob, idx, prompt, ntok, act_mode):
 
 
 if __name__ == "__main__":
-    sys.exit(main())
+    # A run that succeeds returns from the script instead of calling sys.exit(0): when
+    # rocprofv3 profiles a process that made a cooperative launch, the process ends in a
+    # segmentation fault inside exit(), in the libraries' exit handlers; on the normal-return
+    # path the profiler's own exit handler writes its records before that, on the sys.exit
+    # path after it (so the records were lost).  Nothing of this library runs at exit.
+    rc = main()
+    if rc:
+        sys.exit(rc)
