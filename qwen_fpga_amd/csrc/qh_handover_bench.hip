@@ -1,0 +1,201 @@
+// qh_handover_bench: the cost of the persistent kernel's hand-over between
+// workgroups on this GPU, measured in isolation (no weights, no arithmetic).
+//
+//   qwen_fpga_amd/bin/qh_handover_bench [rounds]
+//
+// 1. ping-pong: two workgroups alternately store a 32-bit tag with a
+//    device-coherent store (sc1) and poll the other's with device-coherent loads
+//    -- the one-way latency of a hand-over between two workgroups, on one XCD
+//    and across XCDs (workgroup b runs on XCD b % 8; checked with HW_REG_XCC_ID).
+// 2. all-to-all: G workgroups each publish 1024 / G of a 1024-value vector as
+//    8-byte {value, tag} pairs (the TagIO layout of qh_stages.hpp: one 64-bit
+//    store per pair) and every workgroup waits until it holds all 1024 current
+//    pairs, its W waves polling a share each; then a workgroup barrier, and the
+//    next round uses the next tag.  Reports microseconds per round, the
+//    hand-over floor of one decode stage (126 such exchanges per token).
+//
+// Every wait has a poll limit; a run that hits it prints ABORT and exits.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <vector>
+
+namespace {
+
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+constexpr int kSc1 = 16;   // device-coherent: bypasses the non-coherent L1 (sc1)
+constexpr unsigned kLimit = 1u << 22;
+
+#define CHECK(x)                                                                      \
+  do {                                                                                \
+    hipError_t e_ = (x);                                                              \
+    if (e_ != hipSuccess) {                                                           \
+      std::fprintf(stderr, "HIP error %s at %s:%d\n", hipGetErrorString(e_), __FILE__, __LINE__); \
+      std::exit(1);                                                                   \
+    }                                                                                 \
+  } while (0)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7ffffff0, 0x00020000);
+}
+__device__ __forceinline__ unsigned xcc_id() {
+  unsigned v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return v & 0xf;
+}
+
+__global__ void xcc_map(unsigned* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
+}
+
+// Workgroups 0 and `peer`, one lane each; every other workgroup exits at once.
+__global__ void pingpong(uint32_t* flags, int iters, int peer, unsigned long long* ticks, int* abort_flag) {
+  const int b = blockIdx.x;
+  if (threadIdx.x != 0 || (b != 0 && b != peer)) return;
+  const auto rs = rsrc(flags);
+  const int mine = b == 0 ? 0 : 64, theirs = b == 0 ? 64 : 0;   // separate 256-byte lines
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  for (int i = 1; i <= iters; ++i) {
+    if (b == 0) __builtin_amdgcn_raw_buffer_store_b32((uint32_t)i, rs, mine * 4, 0, kSc1);
+    unsigned p = 0;
+    while (true) {
+      asm volatile("" ::: "memory");   // a new load every iteration
+      if (__builtin_amdgcn_raw_buffer_load_b32(rs, theirs * 4, 0, kSc1) == (uint32_t)i) break;
+      if (++p > kLimit) {
+        *abort_flag = 1;
+        return;
+      }
+    }
+    if (b != 0) __builtin_amdgcn_raw_buffer_store_b32((uint32_t)i, rs, mine * 4, 0, kSc1);
+  }
+  if (b == 0) ticks[0] = __builtin_amdgcn_s_memrealtime() - t0;
+}
+
+// All-to-all of 1024 pairs among the workgroups with member[b] >= 0 (G of them).
+__global__ void all_to_all(u32x2* vec, const int* member, int G, int rounds, int* abort_flag,
+                           unsigned long long* ticks) {
+  const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, W = blockDim.x >> 6;
+  const int m = member[b];
+  if (m < 0) return;
+  const int per = 1024 / G;   // pairs published by each member
+  const auto rs = rsrc(vec);
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  for (int r = 1; r <= rounds; ++r) {
+    const int buf = (r & 1) * 1024;   // two buffers: a round's pairs are not overwritten while read
+    for (int e = t; e < per; e += blockDim.x) {
+      u32x2 p;
+      p[0] = (uint32_t)(m * per + e);
+      p[1] = (uint32_t)r;
+      __builtin_amdgcn_raw_buffer_store_b64(p, rs, (buf + m * per + e) * 8, 0, kSc1);
+    }
+    // wave w polls pairs [w * 1024 / W, (w + 1) * 1024 / W), 16 bytes (two pairs) per lane per load
+    const int lo = (t >> 6) * (1024 / W), n = 1024 / W;
+    unsigned p = 0;
+    while (true) {
+      asm volatile("" ::: "memory");   // a new load every iteration
+      bool ok = true;
+      for (int i = 2 * lane; i < n; i += 128) {
+        const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rs, (buf + lo + i) * 8, 0, kSc1);
+        ok = ok & (u[1] == (uint32_t)r) & (u[3] == (uint32_t)r);
+      }
+      if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+      if (++p > kLimit) {
+        __hip_atomic_store(abort_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      if ((p & 255u) == 0 && __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+    }
+    __syncthreads();
+    if (__hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;
+  }
+  if (t == 0) ticks[b] = __builtin_amdgcn_s_memrealtime() - t0;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  const int rounds = argc > 1 ? std::atoi(argv[1]) : 2000;
+  if (rounds < 1 || rounds > 1000000) {
+    std::fprintf(stderr, "rounds must be 1 .. 1000000\n");
+    return 2;
+  }
+  int dev = 0, ncu = 0;
+  CHECK(hipGetDevice(&dev));
+  CHECK(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
+  const int nblk = ncu < 256 ? ncu : 256;
+  unsigned* map;
+  CHECK(hipMalloc(&map, sizeof(unsigned) * nblk));
+  hipLaunchKernelGGL(xcc_map, dim3(nblk), dim3(64), 0, 0, map);
+  CHECK(hipDeviceSynchronize());
+  std::vector<unsigned> xcc(nblk);
+  CHECK(hipMemcpy(xcc.data(), map, sizeof(unsigned) * nblk, hipMemcpyDeviceToHost));
+  int off = 0;
+  for (int i = 0; i < nblk; ++i) off += xcc[i] != (unsigned)(i % 8);
+  std::printf("workgroups: %d; workgroups not on XCD b %% 8: %d\n", nblk, off);
+
+  uint32_t* flags;
+  int* abort_flag;
+  unsigned long long* ticks;
+  u32x2* vec;
+  int* member;
+  CHECK(hipMalloc(&flags, 1024));
+  CHECK(hipMalloc(&abort_flag, sizeof(int)));
+  CHECK(hipMalloc(&ticks, sizeof(unsigned long long) * 256));
+  CHECK(hipMalloc(&vec, sizeof(u32x2) * 2048));
+  CHECK(hipMalloc(&member, sizeof(int) * 256));
+  auto reset = [&]() {
+    CHECK(hipMemset(flags, 0, 1024));
+    CHECK(hipMemset(abort_flag, 0, sizeof(int)));
+    CHECK(hipMemset(ticks, 0, sizeof(unsigned long long) * 256));
+    CHECK(hipMemset(vec, 0, sizeof(u32x2) * 2048));
+    CHECK(hipDeviceSynchronize());
+  };
+  auto aborted = [&]() {
+    int a = 0;
+    CHECK(hipMemcpy(&a, abort_flag, sizeof(int), hipMemcpyDeviceToHost));
+    return a != 0;
+  };
+  // s_memrealtime counts at 100 MHz
+  const double tick_ns = 10.0;
+
+  for (int peer : {8, 1, 128}) {   // same XCD, neighbouring XCD, far workgroup
+    if (peer >= nblk) continue;
+    reset();
+    hipLaunchKernelGGL(pingpong, dim3(nblk), dim3(64), 0, 0, flags, rounds, peer, ticks, abort_flag);
+    CHECK(hipDeviceSynchronize());
+    unsigned long long tk = 0;
+    CHECK(hipMemcpy(&tk, ticks, sizeof tk, hipMemcpyDeviceToHost));
+    std::printf("ping-pong workgroup 0 <-> %d (%s XCD): %.1f ns one way%s\n", peer,
+                xcc[peer] == xcc[0] ? "same" : "other", tk * tick_ns / (2.0 * rounds), aborted() ? " ABORT" : "");
+  }
+
+  struct Case {
+    int G, W;
+    bool same_xcd;
+  };
+  const Case cases[] = {{256, 1, false}, {256, 2, false}, {256, 4, false}, {256, 8, false}, {64, 4, false},
+                        {32, 4, false},  {32, 4, true},   {8, 4, true},    {2, 4, false}};
+  for (const Case& c : cases) {
+    if (c.G > nblk) continue;
+    std::vector<int> mem(nblk, -1);
+    int k = 0;
+    for (int b = 0; b < nblk && k < c.G; ++b)
+      if (!c.same_xcd || xcc[b] == xcc[0]) mem[b] = k++;
+    if (k < c.G) continue;
+    CHECK(hipMemcpy(member, mem.data(), sizeof(int) * nblk, hipMemcpyHostToDevice));
+    reset();
+    hipLaunchKernelGGL(all_to_all, dim3(nblk), dim3(64 * c.W), 0, 0, vec, member, c.G, rounds, abort_flag, ticks);
+    CHECK(hipDeviceSynchronize());
+    std::vector<unsigned long long> tk(nblk);
+    CHECK(hipMemcpy(tk.data(), ticks, sizeof(unsigned long long) * nblk, hipMemcpyDeviceToHost));
+    const unsigned long long mx = *std::max_element(tk.begin(), tk.end());
+    std::printf("all-to-all of 1024 tagged pairs, G = %3d workgroups (%s), %d poll waves each: %.3f us per round%s\n",
+                c.G, c.same_xcd ? "one XCD" : "all XCDs", c.W, mx * tick_ns / 1000.0 / rounds,
+                aborted() ? " ABORT" : "");
+    if (aborted()) return 1;
+  }
+  return 0;
+}
