@@ -351,11 +351,24 @@ def _attention_f64(q, kc, vc, Tn):
     return og
 
 
-def test_attention_against_float64(orc, blob, entries):
-    """The attention layer (both orders) against textbook float64 softmax attention with the
-    GQA map kv = h // 4 (the two kv heads hold different data, so a wrong map fails), on the
-    same projections, QK-norm and RoPE, followed by the gate and o_proj in float64."""
-    L = orc.lib()
+def _attention_layer_f64(L, qg, qn, ow, osc, kc, vc, Tpast):
+    """The attention layer's output in float64 from its q/gate projection `qg` and the cache rows
+    0..Tpast (row Tpast = the current token's k/v, as the layer wrote it): QK-norm and RoPE of q at
+    position Tpast, textbook softmax attention, the sigmoid gate, o_proj."""
+    c, s = np.empty(64, np.float32), np.empty(64, np.float32)
+    L.or_rope_cos_sin(Tpast, p(c), p(s))
+    qh = np.empty((8, 256), np.float32)
+    for h in range(8):
+        y = np.empty(256, np.float32)
+        L.or_rmsnorm(p(y), p(f32(qg[h * 512:h * 512 + 256])), p(qn), 256, 1e-6)
+        L.or_apply_rope(p(y), p(c), p(s))
+        qh[h] = y
+    gate = qg.reshape(8, 512)[:, 256:].astype(np.float64)
+    og = _attention_f64(qh, kc, vc, Tpast + 1) / (1.0 + np.exp(-gate))
+    return (ow.astype(np.float64) @ og.reshape(-1)) * osc.astype(np.float64)
+
+
+def _attention_weights(orc, blob, entries):
     T3 = _layer_tensors(orc, blob, entries, 3)
     qp, (qw, qs) = T3("self_attn.q_proj.weight")
     kp, _ = T3("self_attn.k_proj.weight")
@@ -363,11 +376,19 @@ def test_attention_against_float64(orc, blob, entries):
     op, (ow, osc) = T3("self_attn.o_proj.weight")
     _, qn = T3("self_attn.q_norm.weight")
     _, kn = T3("self_attn.k_norm.weight")
+    return (qp, kp, vp, op), (qw, qs, ow, osc, qn, kn)
+
+
+def test_attention_against_float64(orc, blob, entries):
+    """The attention layer (both orders) against textbook float64 softmax attention with the
+    GQA map kv = h // 4 (the two kv heads hold different data, so a wrong map fails), on the
+    same projections, QK-norm and RoPE, followed by the gate and o_proj in float64."""
+    L = orc.lib()
+    (qp, kp, vp, op), (qw, qs, ow, osc, qn, kn) = _attention_weights(orc, blob, entries)
     r = rng(41)
     x = f32(r.standard_normal(1024))
     qg = np.empty(4096, np.float32)
     L.or_gemv_i8(p(qg), p(qw), p(qs), p(x), 4096, 1024)
-    gate = qg.reshape(8, 512)[:, 256:].astype(np.float64)
     for order in (orc.ORDER_REF, orc.ORDER_DEV):
         for Tpast in (0, 37, 700):
             kc = f32(r.standard_normal((Tpast + 1, 512)))
@@ -376,17 +397,35 @@ def test_attention_against_float64(orc, blob, entries):
             k1, v1 = kc.copy(), vc.copy()
             L.or_attention_layer(p(out), p(x), qp, kp, vp, op, p(qn), p(kn), Tpast, p(k1), p(v1), Tpast,
                                  orc.W8A16, order)
-            c, s = np.empty(64, np.float32), np.empty(64, np.float32)
-            L.or_rope_cos_sin(Tpast, p(c), p(s))
-            qh = np.empty((8, 256), np.float32)
-            for h in range(8):
-                y = np.empty(256, np.float32)
-                L.or_rmsnorm(p(y), p(f32(qg[h * 512:h * 512 + 256])), p(qn), 256, 1e-6)
-                L.or_apply_rope(p(y), p(c), p(s))
-                qh[h] = y
-            og = _attention_f64(qh, k1, v1, Tpast + 1) / (1.0 + np.exp(-gate))
-            exp_out = (ow.astype(np.float64) @ og.reshape(-1)) * osc.astype(np.float64)
+            exp_out = _attention_layer_f64(L, qg, qn, ow, osc, k1, v1, Tpast)
             assert_close(out, exp_out, rtol=1e-3, atol=1e-3, what=f"attention T={Tpast} order={order}")
+
+
+@pytest.mark.parametrize("T", [4095, 32767])
+def test_twin_long_context_against_float64(orc, blob, entries, T):
+    """The device twin (ORDER_DEV: split-K flash decoding with an online softmax) at contexts
+    4096 and 32768, on exactly the inputs with which the GPU test of the attention layer checks
+    the device bit for bit against this twin (seed T, x and the KV cache ~ N(0,1)), against
+    float64 brute force.  The tolerance is relative to the output's own magnitude, since long
+    contexts average the values down: 2e-5 of max|out| elementwise (the twin is within 1.6e-6)."""
+    L = orc.lib()
+    (qp, kp, vp, op), (qw, qs, ow, osc, qn, kn) = _attention_weights(orc, blob, entries)
+    r = rng(T)
+    x = f32(r.standard_normal(1024))
+    kc = f32(r.standard_normal((T + 1, 512)))
+    vc = f32(r.standard_normal((T + 1, 512)))
+    out, k1, v1 = np.empty(1024, np.float32), kc.copy(), vc.copy()
+    L.or_attention_layer(p(out), p(x), qp, kp, vp, op, p(qn), p(kn), T, p(k1), p(v1), T, orc.W8A16, orc.ORDER_DEV)
+    qg = np.empty(4096, np.float32)
+    L.or_gemv_i8(p(qg), p(qw), p(qs), p(x), 4096, 1024)
+    exp_out = _attention_layer_f64(L, qg, qn, ow, osc, k1, v1, T)
+    scale = np.abs(exp_out).max()
+    err = np.abs(out.astype(np.float64) - exp_out).max()
+    assert err <= 2e-5 * scale, f"T={T}: max err {err:.3g} vs max|out| {scale:.3g}"
+    # the current token's k/v landed in row T; the past rows are untouched
+    assert_bitwise(k1[:T], kc[:T], "past keys")
+    assert_bitwise(v1[:T], vc[:T], "past values")
+    assert not np.array_equal(k1[T], kc[T])
 
 
 def test_rope_is_a_rotation(orc):
