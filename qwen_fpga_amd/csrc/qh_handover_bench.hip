@@ -74,25 +74,26 @@ __global__ void pingpong(uint32_t* flags, int iters, int peer, unsigned long lon
   if (b == 0) ticks[0] = __builtin_amdgcn_s_memrealtime() - t0;
 }
 
-// All-to-all of 1024 pairs among the workgroups with member[b] >= 0 (G of them).
-__global__ void all_to_all(u32x2* vec, const int* member, int G, int rounds, int* abort_flag,
+// All-to-all of N pairs (N a multiple of 128 and of G) among the workgroups
+// with member[b] >= 0 (G of them).
+__global__ void all_to_all(u32x2* vec, const int* member, int G, int N, int rounds, int* abort_flag,
                            unsigned long long* ticks) {
   const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, W = blockDim.x >> 6;
   const int m = member[b];
   if (m < 0) return;
-  const int per = 1024 / G;   // pairs published by each member
+  const int per = N / G;   // pairs published by each member
   const auto rs = rsrc(vec);
   const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
   for (int r = 1; r <= rounds; ++r) {
-    const int buf = (r & 1) * 1024;   // two buffers: a round's pairs are not overwritten while read
+    const int buf = (r & 1) * N;   // two buffers: a round's pairs are not overwritten while read
     for (int e = t; e < per; e += blockDim.x) {
       u32x2 p;
       p[0] = (uint32_t)(m * per + e);
       p[1] = (uint32_t)r;
       __builtin_amdgcn_raw_buffer_store_b64(p, rs, (buf + m * per + e) * 8, 0, kSc1);
     }
-    // wave w polls pairs [w * 1024 / W, (w + 1) * 1024 / W), 16 bytes (two pairs) per lane per load
-    const int lo = (t >> 6) * (1024 / W), n = 1024 / W;
+    // wave w polls pairs [w * N / W, (w + 1) * N / W), 16 bytes (two pairs) per lane per load
+    const int lo = (t >> 6) * (N / W), n = N / W;
     unsigned p = 0;
     while (true) {
       asm volatile("" ::: "memory");   // a new load every iteration
@@ -110,6 +111,71 @@ __global__ void all_to_all(u32x2* vec, const int* member, int G, int rounds, int
     }
     __syncthreads();
     if (__hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;
+  }
+  if (t == 0) ticks[b] = __builtin_amdgcn_s_memrealtime() - t0;
+}
+
+
+// Two-level all-to-all of 1024 pairs over all 256 workgroups, grouped into 8
+// groups of 32 (group of workgroup b: b % 8, its XCD, when `by_xcd`; else
+// b / 32, a group spread over every XCD).  Level 1: the first F members of a
+// group each fetch 1024 / F pairs from the global vector with wave 0 and
+// republish them into the group's own copy; level 2: every member's W waves
+// poll the group's copy, as in all_to_all.
+__global__ void two_level(u32x2* vec, u32x2* grp, int F, int by_xcd, int rounds, int* abort_flag,
+                          unsigned long long* ticks) {
+  const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, W = blockDim.x >> 6;
+  const int g = by_xcd ? (b & 7) : (b >> 5), j = by_xcd ? (b >> 3) : (b & 31);   // group, rank in it
+  const auto rs = rsrc(vec), rg = rsrc(grp);
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  bool stop = false;
+  for (int r = 1; r <= rounds && !stop; ++r) {
+    const int buf = (r & 1) * 1024;
+    if (t < 4) {   // publish pairs 4b .. 4b + 3
+      u32x2 p;
+      p[0] = (uint32_t)(4 * b + t);
+      p[1] = (uint32_t)r;
+      __builtin_amdgcn_raw_buffer_store_b64(p, rs, (buf + 4 * b + t) * 8, 0, kSc1);
+    }
+    const int gbase = ((r & 1) * 8 + g) * 1024;
+    if (j < F && t < 64) {   // level 1: pairs [j * n1, (j + 1) * n1), two per lane
+      const int n1 = 1024 / F;
+      const int i = j * n1 + 2 * lane;
+      const bool mine = 2 * lane < n1;
+      unsigned p = 0;
+      u32x4 u;
+      while (true) {
+        asm volatile("" ::: "memory");
+        u = __builtin_amdgcn_raw_buffer_load_b128(rs, (buf + (mine ? i : j * n1)) * 8, 0, kSc1);
+        if (__builtin_amdgcn_ballot_w64(mine && (u[1] != (uint32_t)r || u[3] != (uint32_t)r)) == 0) break;
+        if (++p > kLimit) {
+          __hip_atomic_store(abort_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        if ((p & 255u) == 0 && __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+      }
+      if (mine) __builtin_amdgcn_raw_buffer_store_b128(u, rg, (gbase + i) * 8, 0, kSc1);
+    }
+    {   // level 2: wave w polls the group copy's pairs [w * 1024 / W, (w + 1) * 1024 / W)
+      const int lo = (t >> 6) * (1024 / W), n = 1024 / W;
+      unsigned p = 0;
+      while (true) {
+        asm volatile("" ::: "memory");
+        bool ok = true;
+        for (int i = 2 * lane; i < n; i += 128) {
+          const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rg, (gbase + lo + i) * 8, 0, kSc1);
+          ok = ok & (u[1] == (uint32_t)r) & (u[3] == (uint32_t)r);
+        }
+        if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+        if (++p > kLimit) {
+          __hip_atomic_store(abort_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        if ((p & 255u) == 0 && __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+      }
+    }
+    __syncthreads();
+    stop = __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
   }
   if (t == 0) ticks[b] = __builtin_amdgcn_s_memrealtime() - t0;
 }
@@ -144,13 +210,13 @@ int main(int argc, char** argv) {
   CHECK(hipMalloc(&flags, 1024));
   CHECK(hipMalloc(&abort_flag, sizeof(int)));
   CHECK(hipMalloc(&ticks, sizeof(unsigned long long) * 256));
-  CHECK(hipMalloc(&vec, sizeof(u32x2) * 2048));
+  CHECK(hipMalloc(&vec, sizeof(u32x2) * 2 * 4096));
   CHECK(hipMalloc(&member, sizeof(int) * 256));
   auto reset = [&]() {
     CHECK(hipMemset(flags, 0, 1024));
     CHECK(hipMemset(abort_flag, 0, sizeof(int)));
     CHECK(hipMemset(ticks, 0, sizeof(unsigned long long) * 256));
-    CHECK(hipMemset(vec, 0, sizeof(u32x2) * 2048));
+    CHECK(hipMemset(vec, 0, sizeof(u32x2) * 2 * 4096));
     CHECK(hipDeviceSynchronize());
   };
   auto aborted = [&]() {
@@ -175,9 +241,12 @@ int main(int argc, char** argv) {
   struct Case {
     int G, W;
     bool same_xcd;
+    int N;
   };
-  const Case cases[] = {{256, 1, false}, {256, 2, false}, {256, 4, false}, {256, 8, false}, {64, 4, false},
-                        {32, 4, false},  {32, 4, true},   {8, 4, true},    {2, 4, false}};
+  const Case cases[] = {{256, 1, false, 1024}, {256, 2, false, 1024}, {256, 4, false, 1024}, {256, 8, false, 1024},
+                        {64, 4, false, 1024},  {32, 4, false, 1024},  {32, 4, true, 1024},   {8, 4, true, 1024},
+                        {2, 4, false, 1024},   {256, 4, false, 512},  {256, 4, false, 2048}, {256, 4, false, 3584},
+                        {256, 8, false, 3584}};
   for (const Case& c : cases) {
     if (c.G > nblk) continue;
     std::vector<int> mem(nblk, -1);
@@ -187,15 +256,37 @@ int main(int argc, char** argv) {
     if (k < c.G) continue;
     CHECK(hipMemcpy(member, mem.data(), sizeof(int) * nblk, hipMemcpyHostToDevice));
     reset();
-    hipLaunchKernelGGL(all_to_all, dim3(nblk), dim3(64 * c.W), 0, 0, vec, member, c.G, rounds, abort_flag, ticks);
+    hipLaunchKernelGGL(all_to_all, dim3(nblk), dim3(64 * c.W), 0, 0, vec, member, c.G, c.N, rounds, abort_flag,
+                       ticks);
     CHECK(hipDeviceSynchronize());
     std::vector<unsigned long long> tk(nblk);
     CHECK(hipMemcpy(tk.data(), ticks, sizeof(unsigned long long) * nblk, hipMemcpyDeviceToHost));
     const unsigned long long mx = *std::max_element(tk.begin(), tk.end());
-    std::printf("all-to-all of 1024 tagged pairs, G = %3d workgroups (%s), %d poll waves each: %.3f us per round%s\n",
-                c.G, c.same_xcd ? "one XCD" : "all XCDs", c.W, mx * tick_ns / 1000.0 / rounds,
+    std::printf("all-to-all of %4d tagged pairs, G = %3d workgroups (%s), %d poll waves each: %.3f us per round%s\n",
+                c.N, c.G, c.same_xcd ? "one XCD" : "all XCDs", c.W, mx * tick_ns / 1000.0 / rounds,
                 aborted() ? " ABORT" : "");
     if (aborted()) return 1;
+  }
+  if (nblk == 256) {
+    u32x2* grp;
+    CHECK(hipMalloc(&grp, sizeof(u32x2) * 2 * 8 * 1024));
+    struct Case2 {
+      int F, by_xcd;
+    };
+    for (const Case2& c : {Case2{32, 1}, Case2{8, 1}, Case2{32, 0}, Case2{8, 0}}) {   // 1024 / F <= 128: one wave load
+      reset();
+      CHECK(hipMemset(grp, 0, sizeof(u32x2) * 2 * 8 * 1024));
+      hipLaunchKernelGGL(two_level, dim3(nblk), dim3(256), 0, 0, vec, grp, c.F, c.by_xcd, rounds, abort_flag, ticks);
+      CHECK(hipDeviceSynchronize());
+      std::vector<unsigned long long> tk(nblk);
+      CHECK(hipMemcpy(tk.data(), ticks, sizeof(unsigned long long) * nblk, hipMemcpyDeviceToHost));
+      const unsigned long long mx = *std::max_element(tk.begin(), tk.end());
+      std::printf("two-level all-to-all, 256 workgroups in 8 groups of 32 (%s), %2d fetchers per group, "
+                  "4 poll waves: %.3f us per round%s\n",
+                  c.by_xcd ? "one XCD each" : "spread over XCDs", c.F, mx * tick_ns / 1000.0 / rounds,
+                  aborted() ? " ABORT" : "");
+      if (aborted()) return 1;
+    }
   }
   return 0;
 }
