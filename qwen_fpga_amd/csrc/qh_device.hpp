@@ -243,6 +243,7 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
 // pointer must be the same on every lane of the wave.  Weights and state that
 // one workgroup owns use ordinary accesses.
 constexpr int kSc1 = 16;   // cache-policy operand: sc1
+constexpr int kNt = 2;     // cache-policy operand: nt (non-temporal)
 
 // A buffer descriptor sits in scalar registers.  Every base address that
 // builds one here is the same on all lanes of the wave (a kernel argument or a

@@ -870,7 +870,10 @@ __device__ __forceinline__ void load_batch(const Seg& g, int row0, int K, int nc
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int c = min(lane + 64 * j, nchunk - 1);
-      const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rw, roff + 16 * c, 0, 0);
+      // non-temporal: a weight byte is read once per token, and 503 MB of them
+      // would otherwise evict from the 256 MB Infinity Cache what is read again
+      // soon (the LM head, the recurrent state, the KV cache)
+      const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rw, roff + 16 * c, 0, kNt);
       w[j][r][0] = t[0];
       w[j][r][1] = t[1];
       w[j][r][2] = t[2];
@@ -1205,6 +1208,7 @@ __device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
 // unconditionally: a batch beyond the last one goes through empty descriptors
 // (no memory access, reads 0), so the loop keeps no conditionally loaded
 // registers and the compiler waits for exactly the batch it consumes.
+template <int POL>
 __device__ __forceinline__ void head_load(const HeadArgs& a, int b, int total, int lane, int rl, uint32_t (&w)[8][4],
                                           float& sc) {
   b = __builtin_amdgcn_readfirstlane(b);   // wave-uniform: scalar descriptors
@@ -1214,7 +1218,7 @@ __device__ __forceinline__ void head_load(const HeadArgs& a, int b, int total, i
   const int bb = in ? b : 0;
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
-    const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rw, (bb * 8 + r) * 1024 + 16 * lane, 0, 0);
+    const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rw, (bb * 8 + r) * 1024 + 16 * lane, 0, POL);
     w[r][0] = t[0];
     w[r][1] = t[1];
     w[r][2] = t[2];
@@ -1236,8 +1240,8 @@ __device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, 
   io.stage_issue(a.h, 1024, vh);
   uint32_t w0[8][4], w1[8][4];
   float sc0 = 0.0f, sc1 = 0.0f;
-  head_load(a, b, total, lane, rl, w0, sc0);   // two batches in flight before the norm prologue
-  head_load(a, b + stride, total, lane, rl, w1, sc1);
+  head_load<kNt>(a, b, total, lane, rl, w0, sc0);   // two batches in flight before the norm prologue
+  head_load<0>(a, b + stride, total, lane, rl, w1, sc1);
   float xv[16], nw[16];
   if (a.nw_lanes)
     load16c(a.nw, lane, nw);
@@ -1260,13 +1264,13 @@ __device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, 
   // before the reduction.  Both halves of the loop body run unconditionally (a
   // wave with an odd number of batches finishes in the tail), so the buffers
   // keep fixed registers and each wait covers exactly the batch consumed.
-  auto batch = [&](int bb, uint32_t (&w)[8][4], float& sc) {
+  auto batch = [&](auto pol, int bb, uint32_t (&w)[8][4], float& sc) {
     float p[8];
 #pragma unroll
     for (int r = 0; r < 8; ++r) p[r] = dot16_i8f(w[r], xv, 0.0f);
     float scur;   // an explicit copy frees sc's register for the next load (no copy at the loop latch)
     asm volatile("v_mov_b32 %0, %1" : "=v"(scur) : "v"(sc));
-    head_load(a, bb + 2 * stride, total, lane, rl, w, sc);
+    head_load<decltype(pol)::value>(a, bb + 2 * stride, total, lane, rl, w, sc);
     const float y = reduce8(p, lane) * scur;
     const int row = bb * 8 + rl;
     if ((lane & 7) == 0) {
@@ -1274,11 +1278,13 @@ __device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, 
       better(bv, bi, y, row);
     }
   };
+  using Nt = std::integral_constant<int, kNt>;
+  using Keep = std::integral_constant<int, 0>;
   for (; b + stride < total; b += 2 * stride) {
-    batch(b, w0, sc0);
-    batch(b + stride, w1, sc1);
+    batch(Nt{}, b, w0, sc0);
+    batch(Keep{}, b + stride, w1, sc1);
   }
-  if (b < total) batch(b, w0, sc0);
+  if (b < total) batch(Nt{}, b, w0, sc0);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     const float ov = __shfl_xor(bv, off, 64);
