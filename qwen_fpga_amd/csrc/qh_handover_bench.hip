@@ -180,6 +180,79 @@ __global__ void two_level(u32x2* vec, u32x2* grp, int F, int by_xcd, int rounds,
   if (t == 0) ticks[b] = __builtin_amdgcn_s_memrealtime() - t0;
 }
 
+
+// The all-to-all of 1024 pairs among 256 workgroups of 4 waves (as all_to_all)
+// while the waves also stream weights, as a decode GEMV stage does: mode 0 no
+// weights; 1: each wave issues 8 KiB of weight loads (8 x 16 bytes per lane),
+// then its first poll; 2: its first poll, then the weight loads (the decode
+// kernel's order; repolls queue behind the weights); 3: waves 0-1 poll half the
+// vector each and waves 2-3 load 16 KiB of weights each (the weight stream kept
+// off the polling waves).  The weights are folded into one value per lane once
+// the vector is complete (where the dot products would use them); they rotate
+// through a buffer larger than the Infinity Cache, so every round reads HBM.
+__global__ void a2a_weights(u32x2* vec, const u32x4* wbuf, unsigned wunits, int mode, int rounds, int* abort_flag,
+                            unsigned long long* ticks, uint32_t* sink) {
+  const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6, nblk = gridDim.x;
+  const auto rs = rsrc(vec);
+  const bool polls = mode != 3 || wave < 2;
+  const int nw = mode == 0 ? 0 : mode == 3 ? (wave < 2 ? 0 : 16) : 8;   // weight loads per lane
+  const int np = mode == 3 ? 4 : 2;                                     // poll loads per lane
+  const int lo = mode == 3 ? wave * 512 : wave * 256;
+  uint32_t acc = 0;
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  bool stop = false;
+  for (int r = 1; r <= rounds && !stop; ++r) {
+    const int buf = (r & 1) * 1024;
+    if (t < 4) {
+      u32x2 p;
+      p[0] = (uint32_t)(4 * b + t);
+      p[1] = (uint32_t)r;
+      __builtin_amdgcn_raw_buffer_store_b64(p, rs, (buf + 4 * b + t) * 8, 0, kSc1);
+    }
+    const unsigned wbase = (unsigned)(((size_t)r * nblk * 4 + b * 4 + wave) * 16 * 64 % wunits);
+    u32x4 wv[16];
+    u32x4 u[4];
+    auto issue_weights = [&]() {
+#pragma unroll
+      for (int k = 0; k < 16; ++k)
+        if (k < nw) wv[k] = wbuf[(wbase + k * 64 + lane) % wunits];
+      asm volatile("" ::: "memory");
+    };
+    auto issue_poll = [&]() {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (k < np) u[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, (buf + lo + 2 * lane + 128 * k) * 8, 0, kSc1);
+      asm volatile("" ::: "memory");
+    };
+    if (mode == 1) issue_weights();
+    if (polls) issue_poll();
+    if (mode == 2 || mode == 3) issue_weights();
+    if (polls) {
+      unsigned p = 0;
+      while (true) {
+        bool ok = true;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (k < np) ok = ok & (u[k][1] == (uint32_t)r) & (u[k][3] == (uint32_t)r);
+        if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+        if (++p > kLimit) {
+          __hip_atomic_store(abort_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        if ((p & 255u) == 0 && __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+        issue_poll();
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+      if (k < nw) acc ^= wv[k][0] ^ wv[k][1] ^ wv[k][2] ^ wv[k][3];
+    __syncthreads();
+    stop = __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+  }
+  if (t == 0) ticks[b] = __builtin_amdgcn_s_memrealtime() - t0;
+  sink[b * blockDim.x + t] = acc;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -268,6 +341,28 @@ int main(int argc, char** argv) {
     if (aborted()) return 1;
   }
   if (nblk == 256) {
+    // the all-to-all with a weight stream beside it
+    const unsigned wunits = 32u << 20;   // 512 MiB of 16-byte units
+    u32x4* wbuf;
+    uint32_t* sink;
+    CHECK(hipMalloc(&wbuf, sizeof(u32x4) * (size_t)wunits));
+    CHECK(hipMemset(wbuf, 1, sizeof(u32x4) * (size_t)wunits));
+    CHECK(hipMalloc(&sink, sizeof(uint32_t) * 256 * 256));
+    const char* what[] = {"no weights", "8 KiB of weights per wave before the first poll",
+                          "8 KiB of weights per wave after the first poll",
+                          "waves 0-1 poll, waves 2-3 load 16 KiB of weights each"};
+    for (int mode = 0; mode < 4; ++mode) {
+      reset();
+      hipLaunchKernelGGL(a2a_weights, dim3(nblk), dim3(256), 0, 0, vec, wbuf, wunits, mode, rounds, abort_flag, ticks,
+                         sink);
+      CHECK(hipDeviceSynchronize());
+      std::vector<unsigned long long> tk(nblk);
+      CHECK(hipMemcpy(tk.data(), ticks, sizeof(unsigned long long) * nblk, hipMemcpyDeviceToHost));
+      const unsigned long long mx = *std::max_element(tk.begin(), tk.end());
+      std::printf("all-to-all of 1024 pairs, 256 workgroups, 4 waves, %s: %.3f us per round%s\n", what[mode],
+                  mx * tick_ns / 1000.0 / rounds, aborted() ? " ABORT" : "");
+      if (aborted()) return 1;
+    }
     u32x2* grp;
     CHECK(hipMalloc(&grp, sizeof(u32x2) * 2 * 8 * 1024));
     struct Case2 {
