@@ -1020,38 +1020,64 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
           for (int e = 0; e < 16; ++e) xv[j][e] = 0.0f;
       }
     }
+    // The norms apply the gains first and 1/rms last: y = (x g) * inv.  Then
+    // the activation maximum needs no second pass over y: rounding is
+    // monotone, so max |fl(u inv)| = fl(max |u| inv) for u = x g, and max |u|
+    // is reduced across the wave together with the sum of squares instead of
+    // after it (golden/model.py:37-45 takes the maximum of y).
+    float amax = 0.0f;   // W8A8: max |y| over the vector, once known
     if constexpr (PRO == P_NORM) {   // norm.hpp:13-20, sum of squares in C16 order
-      float ss = 0.0f;
+      float ss = 0.0f, mu = 0.0f;
 #pragma unroll
       for (int j = 0; j < NCH; ++j)
         if (lane + 64 * j < nchunk) ss = dot16_f32(xv[j], xv[j], ss);
+#pragma unroll
+      for (int j = 0; j < NCH; ++j)
+        if (lane + 64 * j < nchunk)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            xv[j][e] = xv[j][e] * (1.0f + nwv16[j][e]);
+            mu = fmaxf(mu, fabsf(xv[j][e]));
+          }
       ss = xor_sum<64>(ss);
+      if constexpr (MODE == M_W8A8) mu = xor_max<64>(mu);
       const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
 #pragma unroll
       for (int j = 0; j < NCH; ++j)
         if (lane + 64 * j < nchunk)
 #pragma unroll
-          for (int e = 0; e < 16; ++e) xv[j][e] = (xv[j][e] * inv) * (1.0f + nwv16[j][e]);
+          for (int e = 0; e < 16; ++e) xv[j][e] = xv[j][e] * inv;
+      amax = mu * inv;
     } else if constexpr (PRO == P_GATED) {   // heads of 128 = groups of 8 lanes; z holds silu(z)
       float zs[NCH][16];
 #pragma unroll
       for (int j = 0; j < NCH; ++j) load16l(zl + 16 * (lane + 64 * j), zs[j]);
 #pragma unroll
       for (int j = 0; j < NCH; ++j) {
-        float ss = dot16_f32(xv[j], xv[j], 0.0f);
+        float ss = dot16_f32(xv[j], xv[j], 0.0f), mu = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          xv[j][e] = (xv[j][e] * nwv16[j][e]) * zs[j][e];
+          mu = fmaxf(mu, fabsf(xv[j][e]));
+        }
         ss = xor_sum<8>(ss);
+        if constexpr (MODE == M_W8A8) mu = xor_max<8>(mu);   // this head's max |u|
         const float inv = 1.0f / sqrtf(ss / 128.0f + a.eps);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) xv[j][e] = ((xv[j][e] * inv) * nwv16[j][e]) * zs[j][e];
+        for (int e = 0; e < 16; ++e) xv[j][e] = xv[j][e] * inv;
+        amax = fmaxf(amax, mu * inv);
       }
     }
     if constexpr (MODE == M_W8A8) {   // _qa (golden/model.py:37-45)
-      float am = 0.0f;
+      float am = amax;   // P_NORM: already the vector's maximum
+      if constexpr (PRO == P_GATED) am = xor_max<64>(am);   // the maximum over the heads
+      if constexpr (PRO != P_NORM && PRO != P_GATED) {
 #pragma unroll
-      for (int j = 0; j < NCH; ++j)
+        for (int j = 0; j < NCH; ++j)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) am = fmaxf(am, fabsf(xv[j][e]));
-      am = xor_max<64>(am);
+          for (int e = 0; e < 16; ++e) am = fmaxf(am, fabsf(xv[j][e]));
+        am = xor_max<64>(am);
+      }
       xs = quant_scale(am);
       const float rs = 1.0f / xs;
       if constexpr (NCH >= 2) {
@@ -1347,7 +1373,7 @@ __device__ __forceinline__ bool deltanet_gates(const DnArgs& a, int h, int tokv,
 #pragma unroll
     for (int e = 0; e < 16; ++e) xv[e] = t1[0][e];
   }
-  if (a.gx_norm != nullptr) {   // norm.hpp:13-20
+  if (a.gx_norm != nullptr) {   // norm.hpp:13-20, in the GEMV prologue's order (x g) * inv
     float nw[16];
     if (a.lanes)
       load16c(a.gx_norm, lane, nw);
@@ -1357,7 +1383,7 @@ __device__ __forceinline__ bool deltanet_gates(const DnArgs& a, int h, int tokv,
     ss = xor_sum<64>(ss);
     const float inv = 1.0f / sqrtf(ss / 1024.0f + a.eps);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) xv[e] = (xv[e] * inv) * (1.0f + nw[e]);
+    for (int e = 0; e < 16; ++e) xv[e] = (xv[e] * (1.0f + nw[e])) * inv;
   }
   if (a.mode == M_W8A8) {   // _qa (golden/model.py:37-45), dequantised
     float am = 0.0f;
