@@ -438,12 +438,28 @@ hipError_t launch_init_gen(StepCtl* ctl, int tok0, int n_prompt, int n_new, int 
   return hipGetLastError();
 }
 
-__global__ void store_gb_kernel(float* gb, float g, float beta) {
-  gb[0] = g;
-  gb[16] = beta;
+
+// The delta-rule ops' inputs in the layout deltanet_body reads (convd = q | k | v
+// at 0 / 2048 / 4096, gb = g[16] | beta[16]), gathered in one launch: nq
+// elements of q and k, nv of v, nh gates (from g / beta, or the scalars gs /
+// bs when those pointers are null).
+__global__ void dn_gather_kernel(float* convd, float* gb, const float* q, const float* k, const float* v,
+                                 const float* g, const float* beta, float gs, float bs, int nq, int nv, int nh) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < nq) {
+    convd[i] = q[i];
+    convd[2048 + i] = k[i];
+  }
+  if (i < nv) convd[4096 + i] = v[i];
+  if (i < nh) {
+    gb[i] = g != nullptr ? g[i] : gs;
+    gb[16 + i] = beta != nullptr ? beta[i] : bs;
+  }
 }
-hipError_t launch_store_gb(float* gb, float g, float beta, hipStream_t s) {
-  store_gb_kernel<<<1, 1, 0, s>>>(gb, g, beta);
+hipError_t launch_dn_gather(float* convd, float* gb, const float* q, const float* k, const float* v, const float* g,
+                            const float* beta, float gs, float bs, int nq, int nv, int nh, hipStream_t s) {
+  const int n = nq > nv ? nq : nv;
+  dn_gather_kernel<<<(n + 255) / 256, 256, 0, s>>>(convd, gb, q, k, v, g, beta, gs, bs, nq, nv, nh);
   return hipGetLastError();
 }
 

@@ -241,7 +241,8 @@ hipError_t launch_quant_rows(int8_t* q, float* scale, const float* w, int rows, 
 hipError_t launch_quant_rows_bf16(int8_t* q, float* scale, const uint16_t* w, int rows, int cols, hipStream_t s);
 hipError_t launch_set_ints(int* dst, int a, int b, hipStream_t s);
 hipError_t launch_set_int(int* dst, int v, hipStream_t s);
-hipError_t launch_store_gb(float* gb, float g, float beta, hipStream_t s);
+hipError_t launch_dn_gather(float* convd, float* gb, const float* q, const float* k, const float* v, const float* g,
+                            const float* beta, float gs, float bs, int nq, int nv, int nh, hipStream_t s);
 hipError_t launch_set_floats(float* dst, const Floats64& v, int n, hipStream_t s);
 hipError_t launch_bump_pos(StepCtl* ctl, hipStream_t s);
 hipError_t launch_init_gen(StepCtl* ctl, int tok0, int n_prompt, int n_new, int eos, hipStream_t s);

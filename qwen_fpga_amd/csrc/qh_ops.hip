@@ -418,10 +418,7 @@ int qh_delta_rule_head(const float* q, const float* k, const float* v, float g, 
   QH_TRY(sc.alloc(rnd(4 * kConvDim) + rnd(4 * 32)));
   float* convd = sc.take<float>(kConvDim);
   float* gb = sc.take<float>(32);
-  QH_HIP(hipMemcpyAsync(convd, q, 4 * kLK, hipMemcpyDeviceToDevice, s));
-  QH_HIP(hipMemcpyAsync(convd + 2048, k, 4 * kLK, hipMemcpyDeviceToDevice, s));
-  QH_HIP(hipMemcpyAsync(convd + 4096, v, 4 * kLV, hipMemcpyDeviceToDevice, s));
-  QH_HIP(launch_store_gb(gb, g, beta, s));
+  QH_HIP(launch_dn_gather(convd, gb, q, k, v, nullptr, nullptr, g, beta, kLK, kLV, 1, s));
   DnArgs d;
   d.convd = convd;
   d.gb = gb;
@@ -440,11 +437,7 @@ int qh_delta_rule_layer(const float* q, const float* k, const float* v, const fl
   QH_TRY(sc.alloc(rnd(4 * kConvDim) + rnd(4 * 32)));
   float* convd = sc.take<float>(kConvDim);
   float* gb = sc.take<float>(32);
-  QH_HIP(hipMemcpyAsync(convd, q, 4 * 2048, hipMemcpyDeviceToDevice, s));
-  QH_HIP(hipMemcpyAsync(convd + 2048, k, 4 * 2048, hipMemcpyDeviceToDevice, s));
-  QH_HIP(hipMemcpyAsync(convd + 4096, v, 4 * 2048, hipMemcpyDeviceToDevice, s));
-  QH_HIP(hipMemcpyAsync(gb, g, 4 * 16, hipMemcpyDeviceToDevice, s));
-  QH_HIP(hipMemcpyAsync(gb + 16, beta, 4 * 16, hipMemcpyDeviceToDevice, s));
+  QH_HIP(launch_dn_gather(convd, gb, q, k, v, g, beta, 0.0f, 0.0f, 2048, 2048, 16, s));
   DnArgs d;
   d.convd = convd;
   d.gb = gb;
