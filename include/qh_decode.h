@@ -47,7 +47,11 @@ extern "C" {
                             decode (QH_ESTATE) until qh_engine_reset.  The environment
                             variable QH_POLL_LIMIT, read at engine creation, sets the
                             failed polls a wait allows (default 2^20, about a second):
-                            a test hook that forces this path. */
+                            a test hook that forces this path.  A second hook,
+                            QH_TAG_START, starts the persistent kernel's hand-over tags
+                            at that value instead of 1, so that a test reaches the
+                            launch that would run past 2^32 - 1 (the engine then
+                            clears the tagged buffers and restarts the tags at 1). */
 
 /* ---- model dimensions (hls/src/types.hpp:20-44) ----------------------- */
 #define QH_HIDDEN 1024

@@ -68,6 +68,7 @@ struct qh_engine {
   uint64_t* arena = nullptr;     // tagged vectors of the persistent program
   size_t arena_pairs = 0;
   uint32_t tag_next = 1;         // first unused tag (the arena holds only smaller tags)
+  uint32_t tag_start = 1;        // tag_next once the arena is (re)allocated (test hook QH_TAG_START)
   int* abort_dev = nullptr;      // set by a hand-over wait that gave up
   // Lane-interleaved copies of the fp32 vectors a wave reads 16 elements per
   // lane (norm gains, the DeltaNet gate rows): element e of lane l's chunk of
@@ -430,7 +431,7 @@ int ensure_prog(qh_engine* e) {
     QH_TRY(dalloc(&e->arena, cnt.used));
     QH_HIP(hipMemset(e->arena, 0, sizeof(uint64_t) * cnt.used));
     e->arena_pairs = cnt.used;
-    e->tag_next = 1;
+    e->tag_next = e->tag_start;
     v.clear();
     h = Vec{};
   }
@@ -660,6 +661,10 @@ int create(const void* blob, size_t blob_len, const char* idx_text, int max_ctx,
   if (const char* pl = std::getenv("QH_POLL_LIMIT")) {   // test hook: force a hand-over wait to give up
     const long v = std::strtol(pl, nullptr, 10);
     if (v >= 0 && v <= (1L << 20)) e->poll_limit = (unsigned)v;
+  }
+  if (const char* ts = std::getenv("QH_TAG_START")) {   // test hook: start the tags near the wrap
+    const unsigned long long v = std::strtoull(ts, nullptr, 10);
+    if (v >= 1 && v <= 0xFFFFFFFFull) e->tag_start = (uint32_t)v;
   }
   e->nsplit_max = (max_ctx + kAttnSplit - 1) / kAttnSplit;
   e->head_grid = kVocab / (kRowsPerBatch * 4 * 4);   // 4 waves x 4 batches per block

@@ -349,3 +349,33 @@ def test_run_hls_cli(q, blob, idx, engine, tmp_path):
     engine.set_mode(1)
     engine.reset()
     assert [int(t) for t in r2.stdout.split()] == engine.generate([11, 2222, 33333, 44], 12)
+
+
+def test_tag_space_wrap(q, blob, torch_cuda, monkeypatch):
+    """A persistent launch whose tags would run past 2^32 - 1 clears the tagged hand-over buffers
+    and restarts the tags at 1 (qh_engine.hip run_persist).  Forced from the host by starting the
+    tags just below the top (QH_TAG_START): the second of three launches wraps, and the ids,
+    logits and every state buffer equal those of an engine whose tags start at 1."""
+    top = 0xFFFFFFFF - 5000   # launch 1 needs 17 * 256 = 4352 tags, launch 2 another 10 * 256
+    monkeypatch.setenv("QH_TAG_START", str(top))
+    e = q.Engine(blob, max_ctx=64)
+    monkeypatch.delenv("QH_TAG_START")
+    f = q.Engine(blob, max_ctx=64)
+    try:
+        runs = []
+        for eng in (e, f):
+            eng.set_exec(q.EXEC_PERSISTENT)
+            a = eng.generate([11, 2222, 33333, 44, 5, 6, 7, 8], 8)
+            b = eng.generate([a[-1]], 8)
+            am, lg = eng.decode_token(b[-1], want_logits=True)
+            st = [d2h(eng.device_ptr(i), shp) for i, shp in
+                  ((1, (18, 16, 128, 128)), (2, (18, 6144, 4)), (3, (6, 64, 512)), (4, (6, 64, 512)))]
+            runs.append((a, b, am, lg, st))
+        (a1, b1, m1, l1, s1), (a2, b2, m2, l2, s2) = runs
+        assert a1 == a2 and b1 == b2 and m1 == m2
+        assert_bitwise(l1, l2, "logits after the wrap")
+        for x, y, what in zip(s1, s2, ("rec", "conv", "k cache", "v cache")):
+            assert_bitwise(x, y, what)
+    finally:
+        e.close()
+        f.close()
