@@ -243,11 +243,15 @@ int qh_engine_set_mode(qh_engine* e, int mode);
  * function); returns QH_ESTATE if the device cannot run the persistent kernel.
  * If a cooperative launch is refused at run time (another process can hold the
  * device's cooperative-launch resources), the engine switches itself to
- * QH_EXEC_GRAPH and completes the call there; qh_engine_get_exec reports it. */
+ * QH_EXEC_GRAPH and completes the call there: qh_engine_get_exec then reports
+ * QH_EXEC_GRAPH, qh_engine_exec_fallbacks counts the refused launches, and with
+ * QH_VERBOSE=1 in the environment each one is named on stderr. */
 #define QH_EXEC_PERSISTENT 0
 #define QH_EXEC_GRAPH 1
 int qh_engine_set_exec(qh_engine* e, int exec);
 int qh_engine_get_exec(const qh_engine* e);
+/* Cooperative launches refused so far (each switched the engine to QH_EXEC_GRAPH). */
+int qh_engine_exec_fallbacks(const qh_engine* e);
 /* Zero recurrent/conv state, empty KV cache, pos = 0 (state.hpp:24-34). */
 int qh_engine_reset(qh_engine* e);
 /* Decode one token (qwen_top): returns the argmax (ties -> lowest id) in

@@ -234,13 +234,13 @@ static void rmsnorm_gated_o(float* y, const float* x, const float* w, const floa
   for (int i = 0; i < n; ++i) y[i] = x[i] * inv * w[i] * or_silu(z[i], order);
 }
 
-/* The norms the device fuses into a GEMV prologue (the layer-input norms and
- * the gated norm before out_proj) apply the gains first and 1/rms last,
- * y = (x g) * inv, so that the activation maximum of the W8A8 quantization is
- * reduced together with the sum of squares; the reference order (ORDER_REF)
- * keeps norm.hpp's (x inv) g. */
-static void gemv_rmsnorm_o(float* y, const float* x, const float* w, int n, float eps, int order) {
-  if (order != OR_ORDER_DEV) {
+/* In W8A8 the norms the device fuses into a GEMV prologue (the layer-input
+ * norms and the gated norm before out_proj) apply the gains first and 1/rms
+ * last, y = (x g) * inv, so that the activation maximum of the quantization is
+ * reduced together with the sum of squares.  W8A16 and the reference order
+ * (ORDER_REF) keep norm.hpp's (x inv) g. */
+static void gemv_rmsnorm_o(float* y, const float* x, const float* w, int n, float eps, int mode, int order) {
+  if (order != OR_ORDER_DEV || mode != OR_W8A8) {
     rmsnorm_o(y, x, w, n, eps, order);
     return;
   }
@@ -249,8 +249,8 @@ static void gemv_rmsnorm_o(float* y, const float* x, const float* w, int n, floa
   for (int i = 0; i < n; ++i) y[i] = (x[i] * (1.0f + w[i])) * inv;
 }
 static void gemv_rmsnorm_gated_o(float* y, const float* x, const float* w, const float* z, int n, float eps,
-                                 int order) {
-  if (order != OR_ORDER_DEV) {
+                                 int mode, int order) {
+  if (order != OR_ORDER_DEV || mode != OR_W8A8) {
     rmsnorm_gated_o(y, x, w, z, n, eps, order);
     return;
   }
@@ -594,7 +594,7 @@ void or_deltanet_layer(float* out, const float* x, const or_tensor* qkv_w, const
                          o + h * LV);
   }
   for (int h = 0; h < LH; ++h)   /* deltanet.hpp:177-179 */
-    gemv_rmsnorm_gated_o(og + h * LV, o + h * LV, gate_norm_w, z + h * LV, LV, EPS, order);
+    gemv_rmsnorm_gated_o(og + h * LV, o + h * LV, gate_norm_w, z + h * LV, LV, EPS, mode, order);
   act_t act2;
   act_prepare(&act2, og, VALUE_DIM, mode, qbuf, xfbuf);   /* model.py:191 _qa(o) */
   proj_i8(out, out_w, &act2, mode, order);
@@ -840,7 +840,7 @@ static void layers(or_model* m, int l0, int l1, float* h, int mode, int order) {
   for (int layer = l0; layer < l1; ++layer) {   /* qwen_synth.hpp:47-77 */
     for (int i = 0; i < HIDDEN; ++i) r[i] = h[i];
     snprintf(nm, sizeof nm, "layers.%d.input_layernorm.weight", layer);
-    gemv_rmsnorm_o(hn, h, f32_of(m, nm), HIDDEN, EPS, order);
+    gemv_rmsnorm_o(hn, h, f32_of(m, nm), HIDDEN, EPS, mode, order);
     if (is_linear(layer)) {
       snprintf(a, sizeof a, "layers.%d.linear_attn", layer);
 #define T_(s) (snprintf(nm, sizeof nm, "%s." s, a), tensor_of(m, nm))
@@ -869,7 +869,7 @@ static void layers(or_model* m, int l0, int l1, float* h, int mode, int order) {
     for (int i = 0; i < HIDDEN; ++i) h[i] = r[i] + mix[i];
     for (int i = 0; i < HIDDEN; ++i) r[i] = h[i];
     snprintf(nm, sizeof nm, "layers.%d.post_attention_layernorm.weight", layer);
-    gemv_rmsnorm_o(hn, h, f32_of(m, nm), HIDDEN, EPS, order);
+    gemv_rmsnorm_o(hn, h, f32_of(m, nm), HIDDEN, EPS, mode, order);
     snprintf(a, sizeof a, "layers.%d.mlp", layer);
     or_tensor gp = T_("gate_proj.weight"), up = T_("up_proj.weight"), dp = T_("down_proj.weight");
     or_mlp_layer(mix, hn, &gp, &up, &dp, mode, order);

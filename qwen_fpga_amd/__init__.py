@@ -460,6 +460,11 @@ class Engine:
         return int(_lib().qh_engine_get_exec(self._h))
 
     @property
+    def exec_fallbacks(self) -> int:
+        """Cooperative launches refused so far (each switched the engine to EXEC_GRAPH)."""
+        return int(_lib().qh_engine_exec_fallbacks(self._h))
+
+    @property
     def pos(self) -> int:
         return int(_lib().qh_engine_pos(self._h))
 

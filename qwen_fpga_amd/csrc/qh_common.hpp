@@ -12,6 +12,7 @@ inline int hip_status(hipError_t e) { return e == hipSuccess ? QH_OK : (int)e; }
 
 // With QH_VERBOSE=1 in the environment, a failing HIP call is named on stderr.
 int hip_report(hipError_t e, const char* what, const char* file, int line);
+bool verbose();   // QH_VERBOSE is set (read once)
 
 #define QH_TRY(expr)                         \
   do {                                       \

@@ -80,6 +80,7 @@ struct qh_engine {
   float last_launch_ms = 0.0f;
   unsigned poll_limit = 1u << 20;  // failed polls before a hand-over wait gives up (QH_POLL_LIMIT)
   bool broken = false;             // a launch returned QH_EDEVICE: decode refused until reset
+  int fallbacks = 0;               // cooperative launches refused (each switched the engine to the graph path)
 };
 
 namespace {
@@ -441,6 +442,15 @@ int ensure_prog(qh_engine* e) {
   build_layers(e, 0, kLayers, true, B, v, h);
   v.push_back(head_stage(e, B, h, false, (int)v.size(), e->persist_grid));
   if ((int)v.size() >= kTagsPerToken || B.used != e->arena_pairs) return QH_ESTATE;
+  // the persistent kernel compiles each GEMV stage kind for one vector length
+  for (const Stage& st : v) {
+    const int want = st.kind == ST_GEMV_NORM_1x8    ? kHidden
+                     : st.kind == ST_GEMV_GATED_2x1 ? kLH * kLV
+                     : st.kind == ST_GEMV_LOAD_2x1  ? kNH * kHD
+                     : st.kind == ST_GEMV_LOAD_4x1  ? kInter
+                                                    : -1;
+    if (want >= 0 && st.g.K != want) return QH_ESTATE;
+  }
   QH_TRY(dalloc(&e->prog[e->mode], v.size()));
   QH_HIP(hipMemcpy(e->prog[e->mode], v.data(), sizeof(Stage) * v.size(), hipMemcpyHostToDevice));
   e->prog_n = (int)v.size();
@@ -498,11 +508,15 @@ int run_persist(qh_engine* e, int tok0, int n_prompt, int n_new, int eos, bool w
   a.abort_flag = e->abort_dev;
   a.poll_limit = e->poll_limit;
   QH_HIP(hipEventRecord(e->launch_ev[0], s));
-  if (launch_persist(a, e->persist_grid, s) != hipSuccess) {
+  if (const hipError_t le = launch_persist(a, e->persist_grid, s); le != hipSuccess) {
     (void)hipGetLastError();
     if (trace != nullptr) (void)hipFree(trace);
     e->persist_grid = 0;
     e->exec = QH_EXEC_GRAPH;
+    e->fallbacks += 1;
+    if (verbose())
+      std::fprintf(stderr, "[qh] cooperative launch of the persistent kernel refused (%s): engine switched to the graph executor\n",
+                   hipGetErrorString(le));
     return kUseGraph;
   }
   QH_HIP(hipEventRecord(e->launch_ev[1], s));
@@ -777,6 +791,7 @@ int qh_engine_set_exec(qh_engine* e, int exec) {
 }
 
 int qh_engine_get_exec(const qh_engine* e) { return e ? e->exec : QH_EINVAL; }
+int qh_engine_exec_fallbacks(const qh_engine* e) { return e ? e->fallbacks : QH_EINVAL; }
 
 int qh_engine_reset(qh_engine* e) {
   if (!e) return QH_EINVAL;

@@ -368,7 +368,14 @@ int main(int argc, char** argv) {
     struct Case2 {
       int F, by_xcd;
     };
-    for (const Case2& c : {Case2{32, 1}, Case2{8, 1}, Case2{32, 0}, Case2{8, 0}}) {   // 1024 / F <= 128: one wave load
+    for (const Case2& c : {Case2{32, 1}, Case2{8, 1}, Case2{32, 0}, Case2{8, 0}}) {
+      // A level-1 fetcher is one wave with one 16-byte load (two pairs) per lane, so it
+      // covers at most 128 pairs: 1024 / F must not exceed that (and F must divide 1024
+      // and fit in a group of 32), or the group copy would never be complete.
+      if (c.F < 1 || c.F > 32 || 1024 % c.F != 0 || 1024 / c.F > 128) {
+        std::fprintf(stderr, "two-level case with %d fetchers per group is not supported (1024 / F > 128)\n", c.F);
+        return 2;
+      }
       reset();
       CHECK(hipMemset(grp, 0, sizeof(u32x2) * 2 * 8 * 1024));
       hipLaunchKernelGGL(two_level, dim3(nblk), dim3(256), 0, 0, vec, grp, c.F, c.by_xcd, rounds, abort_flag, ticks);

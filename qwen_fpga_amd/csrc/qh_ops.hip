@@ -26,13 +26,17 @@ void rope_row(int pos, float* out64) {
   }
 }
 
+bool verbose() {
+  static const bool v = [] {
+    const char* s = std::getenv("QH_VERBOSE");
+    return s != nullptr && s[0] != '\0' && s[0] != '0';
+  }();
+  return v;
+}
+
 int hip_report(hipError_t e, const char* what, const char* file, int line) {
   if (e == hipSuccess) return QH_OK;
-  static const bool verbose = [] {
-    const char* v = std::getenv("QH_VERBOSE");
-    return v != nullptr && v[0] != '\0' && v[0] != '0';
-  }();
-  if (verbose) std::fprintf(stderr, "[qh] %s:%d: %s -> %s (%d)\n", file, line, what, hipGetErrorString(e), (int)e);
+  if (verbose()) std::fprintf(stderr, "[qh] %s:%d: %s -> %s (%d)\n", file, line, what, hipGetErrorString(e), (int)e);
   return (int)e;
 }
 

@@ -14,6 +14,7 @@
 // argmax of the previous token, which every workgroup computes from the head
 // partials of all workgroups -- by then every workgroup has finished every
 // stage of the previous token, including its reads.
+#include "qh_decode.h"
 #include "qh_stages.hpp"
 
 namespace qh {
@@ -77,10 +78,11 @@ __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistA
       io.tr = tr;
       bool ok;
       switch (st.kind) {
-        case ST_GEMV_NORM_1x8: ok = gemv_body<1, MODE, P_NORM, 8>(st.g, blk, nblk, io, tok); break;
-        case ST_GEMV_GATED_2x1: ok = gemv_body<2, MODE, P_GATED, 1>(st.g, blk, nblk, io, tok); break;
-        case ST_GEMV_LOAD_2x1: ok = gemv_body<2, MODE, P_LOAD, 1>(st.g, blk, nblk, io, tok); break;
-        case ST_GEMV_LOAD_4x1: ok = gemv_body<4, MODE, P_LOAD, 1>(st.g, blk, nblk, io, tok); break;
+        // the vector lengths of the stage kinds are fixed (the engine checks its program)
+        case ST_GEMV_NORM_1x8: ok = gemv_body<1, MODE, P_NORM, 8, QH_HIDDEN>(st.g, blk, nblk, io, tok); break;
+        case ST_GEMV_GATED_2x1: ok = gemv_body<2, MODE, P_GATED, 1, QH_LH * QH_LV>(st.g, blk, nblk, io, tok); break;
+        case ST_GEMV_LOAD_2x1: ok = gemv_body<2, MODE, P_LOAD, 1, QH_NH * QH_HD>(st.g, blk, nblk, io, tok); break;
+        case ST_GEMV_LOAD_4x1: ok = gemv_body<4, MODE, P_LOAD, 1, QH_INTER>(st.g, blk, nblk, io, tok); break;
         case ST_DELTANET: ok = deltanet_all(st.d, blk, nblk, io, tok); break;
         case ST_ATTN: ok = attn_body(st.at, pos, blk, nblk, io); break;
         case ST_COMBINE: ok = combine_body(st.at, pos, blk, io); break;

@@ -850,30 +850,60 @@ __device__ __forceinline__ void gemv_epilogue(const Seg& g, int ost, int lane, i
   }
 }
 
+// A segment descriptor with every field made wave-uniform (scalar registers):
+// the loads, clamps and selects built from it are then scalar instructions, not
+// per-lane address arithmetic on the stage's critical path.
+__device__ __forceinline__ Seg seg_uniform(const Seg& s) {
+  Seg g;
+  g.kind = __builtin_amdgcn_readfirstlane(s.kind);
+  g.epi = __builtin_amdgcn_readfirstlane(s.epi);
+  g.batch0 = __builtin_amdgcn_readfirstlane(s.batch0);
+  g.nbatch = __builtin_amdgcn_readfirstlane(s.nbatch);
+  g.rows = __builtin_amdgcn_readfirstlane(s.rows);
+  g.res_st = __builtin_amdgcn_readfirstlane(s.res_st);
+  g.w = static_cast<const int8_t*>(wave_uniform(s.w));
+  g.sw = static_cast<const float*>(wave_uniform(s.sw));
+  g.wf = static_cast<const float*>(wave_uniform(s.wf));
+  g.w2 = static_cast<const int8_t*>(wave_uniform(s.w2));
+  g.sw2 = static_cast<const float*>(wave_uniform(s.sw2));
+  g.out = static_cast<float*>(wave_uniform(s.out));
+  g.acc_out = static_cast<int32_t*>(wave_uniform(s.acc_out));
+  g.res = static_cast<const float*>(wave_uniform(s.res));
+  g.c0 = static_cast<const float*>(wave_uniform(s.c0));
+  g.c1 = static_cast<const float*>(wave_uniform(s.c1));
+  g.c2 = static_cast<float*>(wave_uniform(s.c2));
+  return g;
+}
+
 // Loads of one batch: every address is clamped into the segment (rows) and the
 // vector (chunks), so the loads are unconditional and issue back to back.  A
 // clamped chunk meets x = 0 (the prologue zeroes chunks beyond K) and a clamped
 // row is never stored, so neither changes a result.  An fp32 segment has no
-// int8 rows: its descriptors are empty and the loads read nothing.
+// int8 rows: its descriptors are empty and the loads read nothing.  g and row0
+// are wave-uniform: a row's byte offset goes in the scalar offset of the
+// buffer load, and only the lane's chunk offset is per lane.
 template <int NCH, int R>
 __device__ __forceinline__ void load_batch(const Seg& g, int row0, int K, int nchunk, int lane,
                                            uint32_t (&w)[NCH][R][4]) {
   const bool pair = g.kind == SEG_PAIR;
   const int n = g.kind == SEG_F32 ? 0 : 0x7ffffff0;
   const int last = g.rows - 1;
+  const __amdgpu_buffer_rsrc_t rw = rsrc_n(g.w, n);
+  const __amdgpu_buffer_rsrc_t rw2 = rsrc_n(pair ? g.w2 : g.w, n);
+  int voff[NCH];
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) voff[j] = 16 * min(lane + 64 * j, nchunk - 1);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int row = __builtin_amdgcn_readfirstlane(min(row0 + r, last));   // wave-uniform
     const bool second = pair && (row & 1);
-    const __amdgpu_buffer_rsrc_t rw = rsrc_n(second ? g.w2 : g.w, n);
-    const int roff = (pair ? (row >> 1) : row) * K;
+    const int roff = __builtin_amdgcn_readfirstlane((pair ? (row >> 1) : row) * K);
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
-      const int c = min(lane + 64 * j, nchunk - 1);
       // non-temporal: a weight byte is read once per token, and 503 MB of them
       // would otherwise evict from the 256 MB Infinity Cache what is read again
       // soon (the LM head, the recurrent state, the KV cache)
-      const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rw, roff + 16 * c, 0, kNt);
+      const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(second ? rw2 : rw, voff[j], roff, kNt);
       w[j][r][0] = t[0];
       w[j][r][1] = t[1];
       w[j][r][2] = t[2];
@@ -882,26 +912,68 @@ __device__ __forceinline__ void load_batch(const Seg& g, int row0, int K, int nc
   }
 }
 
-// Segment of batch b; b is wave-uniform, and readfirstlane makes that visible
-// to the compiler so the descriptor is read with scalar loads.
-__device__ __forceinline__ int seg_of(const GemvArgs& a, int b) {
-  int si = 0;
-  while (si + 1 < a.nseg && b >= a.seg[si + 1].batch0) ++si;
-  return __builtin_amdgcn_readfirstlane(si);
-}
-
 // The quantised activation of a W8A8 GEMV workgroup: [NCH][64 lanes][4 dwords].
 __device__ __forceinline__ uint32_t* gemv_qlds() {
   __shared__ __attribute__((aligned(16))) uint32_t q[4 * 64 * 4];
   return q;
 }
 
-template <int NCH, int MODE, int PRO, int R, class IO>
+// KC: the vector length when the caller knows it at compile time (the
+// persistent kernel's stage kinds), 0 to take it from the descriptor.
+template <int NCH, int MODE, int PRO, int R, int KC = 0, class IO>
 __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, IO& io, int tokv) {
   const int lane = threadIdx.x & 63, nwv = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int K = a.K, nchunk = K >> 4;
-  const int total = a.seg[a.nseg - 1].batch0 + a.seg[a.nseg - 1].nbatch;
+  // The descriptor (a workgroup copy in LDS) is read into registers once, in one
+  // batch of independent reads.  Read through the reference where it is used,
+  // every field after a memory clobber (each poll has one) would be another LDS
+  // read, and chains of them (the segment search, a weight row's matrix) are
+  // dependent round trips on the stage's critical path.
+  const int K = KC != 0 ? KC : __builtin_amdgcn_readfirstlane(a.K);
+  const int nseg = a.nseg;
+  const float* const ax = a.x;
+  const float* const anw = a.nw;
+  const int nw_lanes = a.nw_lanes;
+  const float* const az = a.z;
+  const int8_t* const axq = a.xq;
+  const float* const asx = a.sx;
+  const float eps = a.eps;
+  const int8_t* const aemb = a.emb;
+  const float* const aemb_s = a.emb_s;
+  const int* const atok = a.tok;
+  float* const ah_out = a.h_out;
+  const int x_st = a.x_st, z_st = a.z_st, out_st = a.out_st;
+  const float* const agw = a.gw;
+  const int grows = a.grows;
+  const float* const ag_alog = a.g_alog;
+  const float* const ag_dtb = a.g_dtb;
+  float* const agout = a.gout;
+  int sb0[4], snb[4], skind[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    sb0[i] = a.seg[i].batch0;
+    snb[i] = a.seg[i].nbatch;
+    skind[i] = a.seg[i].kind;
+  }
+  const int nchunk = K >> 4;
+  int total = 0;
+  bool has_f32 = false;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (i < nseg) {
+      total = sb0[i] + snb[i];   // segments are in batch order: the last one ends the range
+      has_f32 = has_f32 || skind[i] == SEG_F32;
+    }
+  total = __builtin_amdgcn_readfirstlane(total);
+  has_f32 = __builtin_amdgcn_readfirstlane((int)has_f32) != 0;
+  // the segment holding batch bb (segments start at increasing batches)
+  auto seg_index = [&](int bb) {
+    int si = 0;
+#pragma unroll
+    for (int i = 1; i < 4; ++i)
+      if (i < nseg && bb >= sb0[i]) si = i;
+    return __builtin_amdgcn_readfirstlane(si);
+  };
   const int stride = nblk * nwv;
   int b = blk * nwv + wave;
 
@@ -912,14 +984,12 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
   // One straight-line block issues every load of the first batch: the first
   // poll of x, the norm gains, the gate row, the weights and the epilogue
   // inputs.  Waves without rows load the workgroup's last batch and drop it.
-  const bool stage_x = PRO != P_LOADQ && !(PRO == P_NORM && a.emb != nullptr);
-  bool has_f32 = false;   // (read before the hand-over wait)
-  for (int i = 0; i < a.nseg; ++i) has_f32 = has_f32 || a.seg[i].kind == SEG_F32;
-  has_f32 = __builtin_amdgcn_readfirstlane((int)has_f32) != 0;
-  const int bq = min(b, total - 1);
-  int si = seg_of(a, bq);
+  const bool stage_x = PRO != P_LOADQ && !(PRO == P_NORM && aemb != nullptr);
   typename IO::VecPoll vx;
-  if constexpr (PRO != P_LOADQ) io.stage_issue(a.x, stage_x ? K : 0, vx);
+  if constexpr (PRO != P_LOADQ) io.stage_issue(ax, stage_x ? K : 0, vx);
+  const int bq = min(b, total - 1);
+  int si = seg_index(bq);
+  Seg g = seg_uniform(a.seg[si]);   // this wave's segment, in scalar registers
   uint32_t w[NCH][R][4];
   EpiAux aux;
   float nwv16[NCH][16];   // norm gains: constants, loaded before the hand-over wait
@@ -927,34 +997,33 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int c = min(lane + 64 * j, nchunk - 1);
-      if (PRO == P_NORM && a.nw_lanes)
-        load16c(a.nw, c, nwv16[j]);   // K = 1024: c = lane
+      if (PRO == P_NORM && nw_lanes)
+        load16c(anw, c, nwv16[j]);   // K = 1024: c = lane
       else
-        load16g(a.nw + (PRO == P_GATED ? ((16 * c) & 127) : 16 * c), nwv16[j]);
+        load16g(anw + (PRO == P_GATED ? ((16 * c) & 127) : 16 * c), nwv16[j]);
     }
   }
   // a DeltaNet gate row (GemvArgs::gw), wave 0 of workgroups nblk - 1 - r
   const int grow = nblk - 1 - blk;
-  const bool gate_wave = PRO == P_NORM && NCH == 1 && wave == 0 && grow < a.grows;
+  const bool gate_wave = PRO == P_NORM && NCH == 1 && wave == 0 && grow < grows;
   float gwv[16];
   float g_alog = 0.0f, g_dtb = 0.0f;   // the head's A_log and dt_bias (g rows only)
   if constexpr (PRO == P_NORM && NCH == 1) {
-    const __amdgpu_buffer_rsrc_t rg = rsrc_n(a.gw, gate_wave ? 0x7ffffff0 : 0);
+    const __amdgpu_buffer_rsrc_t rg = rsrc_n(agw, gate_wave ? 0x7ffffff0 : 0);
     load16c_rs(rg, gate_wave ? grow * 1024 : 0, lane, gwv);
     // constants: loaded with the gate row, ahead of the hand-over wait (empty
     // descriptors read 0 on waves that compute no g)
     const bool g_row = gate_wave && grow >= 16;
-    g_alog = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc_n(a.g_alog, g_row ? 64 : 0),
+    g_alog = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc_n(ag_alog, g_row ? 64 : 0),
                                                                            4 * (grow & 15), 0, 0));
-    g_dtb = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc_n(a.g_dtb, g_row ? 64 : 0),
+    g_dtb = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc_n(ag_dtb, g_row ? 64 : 0),
                                                                           4 * (grow & 15), 0, 0));
   }
   // The weights and epilogue inputs come last: a wave's loads return in issue
   // order, so whatever the prologue reads (x, the norm gains, the gate row)
   // is issued before them and its wait does not include the weights.
   {
-    const Seg& g = a.seg[si];
-    const int row0 = (bq - g.batch0) * R;
+    const int row0 = __builtin_amdgcn_readfirstlane((bq - g.batch0) * R);
     load_batch<NCH, R>(g, row0, K, nchunk, lane, w);   // SEG_F32: never read
     epi_prefetch(g, row0 + row_of_lane<R>(lane), aux, io);
   }
@@ -964,12 +1033,12 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
   const float* zl = nullptr;
   if (stage_x) {
     float* buf = io.slot();
-    if (!io.stage_finish(a.x, a.x_st, K, buf, vx)) return false;
+    if (!io.stage_finish(ax, x_st, K, buf, vx)) return false;
     xl = buf;
   }
   if constexpr (PRO == P_GATED) {
     float* buf = io.slot();
-    if (!io.stage_vec(a.z, a.z_st, K, buf)) return false;
+    if (!io.stage_vec(az, z_st, K, buf)) return false;
     zl = buf;
   }
   io.mark(1);   // trace: input vector in LDS
@@ -979,24 +1048,24 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
   uint32_t xq[NCH][4];   // int8 activation (W8A8)
   float xs = 1.0f;       // activation scale (W8A8)
   if constexpr (PRO == P_LOADQ) {
-    xs = a.sx != nullptr ? *as_global(a.sx) : 1.0f;   // E_ACCI needs no scale
+    xs = asx != nullptr ? *as_global(asx) : 1.0f;   // E_ACCI needs no scale
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int c = lane + 64 * j;
-      load16b(a.xq + 16 * min(c, nchunk - 1), xq[j]);
+      load16b(axq + 16 * min(c, nchunk - 1), xq[j]);
       if (c >= nchunk) xq[j][0] = xq[j][1] = xq[j][2] = xq[j][3] = 0u;
 #pragma unroll
       for (int e = 0; e < 16; ++e) xv[j][e] = i8_at(xq[j], e) * xs;
     }
   } else {
-    if (PRO == P_NORM && a.emb != nullptr) {   // embed_row (gemv.hpp:76-84)
+    if (PRO == P_NORM && aemb != nullptr) {   // embed_row (gemv.hpp:76-84)
       // wave-uniform at once: the wait for the token load then sits here, on
       // this path only (consumed under the lane condition below, the load stayed
       // pending where the paths join and the compiler drained every load there,
       // the weights included)
-      const int tok = __builtin_amdgcn_readfirstlane(a.tok != nullptr ? ldc_i(a.tok) : tokv);
-      const int8_t* er = a.emb + (size_t)tok * K;
-      const float es = as_global(a.emb_s)[tok];
+      const int tok = __builtin_amdgcn_readfirstlane(atok != nullptr ? ldc_i(atok) : tokv);
+      const int8_t* er = aemb + (size_t)tok * K;
+      const float es = as_global(aemb_s)[tok];
 #pragma unroll
       for (int j = 0; j < NCH; ++j) {
         const int c = lane + 64 * j;
@@ -1005,7 +1074,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
           load16b(er + 16 * c, t);
 #pragma unroll
           for (int e = 0; e < 16; ++e) xv[j][e] = i8_at(t, e) * es;
-          if (a.h_out != nullptr && blk == 0 && threadIdx.x < 64) io.st16(a.h_out, a.out_st, 16 * c, xv[j]);
+          if (ah_out != nullptr && blk == 0 && threadIdx.x < 64) io.st16(ah_out, out_st, 16 * c, xv[j]);
         } else {
 #pragma unroll
           for (int e = 0; e < 16; ++e) xv[j][e] = 0.0f;
@@ -1020,33 +1089,41 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
           for (int e = 0; e < 16; ++e) xv[j][e] = 0.0f;
       }
     }
-    // The norms apply the gains first and 1/rms last: y = (x g) * inv.  Then
-    // the activation maximum needs no second pass over y: rounding is
+    // W8A8: the norms apply the gains first and 1/rms last, y = (x g) * inv.
+    // Then the activation maximum needs no second pass over y: rounding is
     // monotone, so max |fl(u inv)| = fl(max |u| inv) for u = x g, and max |u|
     // is reduced across the wave together with the sum of squares instead of
-    // after it (golden/model.py:37-45 takes the maximum of y).
+    // after it (golden/model.py:37-45 takes the maximum of y).  W8A16 keeps
+    // norm.hpp's order, (x inv) g.
     float amax = 0.0f;   // W8A8: max |y| over the vector, once known
     if constexpr (PRO == P_NORM) {   // norm.hpp:13-20, sum of squares in C16 order
       float ss = 0.0f, mu = 0.0f;
 #pragma unroll
       for (int j = 0; j < NCH; ++j)
         if (lane + 64 * j < nchunk) ss = dot16_f32(xv[j], xv[j], ss);
+      if constexpr (MODE == M_W8A8) {
+#pragma unroll
+        for (int j = 0; j < NCH; ++j)
+          if (lane + 64 * j < nchunk)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              xv[j][e] = xv[j][e] * (1.0f + nwv16[j][e]);
+              mu = fmaxf(mu, fabsf(xv[j][e]));
+            }
+      }
+      ss = xor_sum<64>(ss);
+      if constexpr (MODE == M_W8A8) mu = xor_max<64>(mu);
+      const float inv = 1.0f / sqrtf(ss / (float)K + eps);
 #pragma unroll
       for (int j = 0; j < NCH; ++j)
         if (lane + 64 * j < nchunk)
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
-            xv[j][e] = xv[j][e] * (1.0f + nwv16[j][e]);
-            mu = fmaxf(mu, fabsf(xv[j][e]));
+            if constexpr (MODE == M_W8A8)
+              xv[j][e] = xv[j][e] * inv;
+            else
+              xv[j][e] = (xv[j][e] * inv) * (1.0f + nwv16[j][e]);
           }
-      ss = xor_sum<64>(ss);
-      if constexpr (MODE == M_W8A8) mu = xor_max<64>(mu);
-      const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
-#pragma unroll
-      for (int j = 0; j < NCH; ++j)
-        if (lane + 64 * j < nchunk)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) xv[j][e] = xv[j][e] * inv;
       amax = mu * inv;
     } else if constexpr (PRO == P_GATED) {   // heads of 128 = groups of 8 lanes; z holds silu(z)
       float zs[NCH][16];
@@ -1055,16 +1132,23 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
 #pragma unroll
       for (int j = 0; j < NCH; ++j) {
         float ss = dot16_f32(xv[j], xv[j], 0.0f), mu = 0.0f;
+        if constexpr (MODE == M_W8A8) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          xv[j][e] = (xv[j][e] * nwv16[j][e]) * zs[j][e];
-          mu = fmaxf(mu, fabsf(xv[j][e]));
+          for (int e = 0; e < 16; ++e) {
+            xv[j][e] = (xv[j][e] * nwv16[j][e]) * zs[j][e];
+            mu = fmaxf(mu, fabsf(xv[j][e]));
+          }
         }
         ss = xor_sum<8>(ss);
         if constexpr (MODE == M_W8A8) mu = xor_max<8>(mu);   // this head's max |u|
-        const float inv = 1.0f / sqrtf(ss / 128.0f + a.eps);
+        const float inv = 1.0f / sqrtf(ss / 128.0f + eps);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) xv[j][e] = xv[j][e] * inv;
+        for (int e = 0; e < 16; ++e) {
+          if constexpr (MODE == M_W8A8)
+            xv[j][e] = xv[j][e] * inv;
+          else
+            xv[j][e] = ((xv[j][e] * inv) * nwv16[j][e]) * zs[j][e];   // norm.hpp:32
+        }
         amax = fmaxf(amax, mu * inv);
       }
     }
@@ -1134,15 +1218,14 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
         val = dev_sigmoid(y);   // beta
       else
         val = -dev_expf(g_alog) * dev_softplus(y + g_dtb);   // g
-      if (lane == 0) io.st1(a.gout, a.out_st, 16 * hh + (grow < 16 ? 1 : 0), val);
+      if (lane == 0) io.st1(agout, out_st, 16 * hh + (grow < 16 ? 1 : 0), val);
     }
   }
   if (b >= total) return true;   // no rows for this wave (it took part in the barriers above)
   const int b0 = b;
   // ---------------- 3. row batches (the next batch's loads overlap this batch's reduction)
   for (; b < total; b += stride) {
-    const Seg& g = a.seg[si];
-    const int row0 = (b - g.batch0) * R;
+    const int row0 = __builtin_amdgcn_readfirstlane((b - g.batch0) * R);
     const int myrow = row0 + row_of_lane<R>(lane);
     float y = 0.0f;
     int acci = 0;
@@ -1193,11 +1276,12 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
     // issue the next batch's loads before reducing this one
     const int bn = b + stride;
     int sin = si;
+    Seg gn = g;
     EpiAux auxn;
     if (bn < total) {
-      sin = seg_of(a, bn);
-      const Seg& gn = a.seg[sin];
-      const int rn = (bn - gn.batch0) * R;
+      sin = seg_index(bn);
+      if (sin != si) gn = seg_uniform(a.seg[sin]);
+      const int rn = __builtin_amdgcn_readfirstlane((bn - gn.batch0) * R);
       if (gn.kind != SEG_F32) load_batch<NCH, R>(gn, rn, K, nchunk, lane, w);
       epi_prefetch(gn, rn + row_of_lane<R>(lane), auxn, io);
     }
@@ -1209,9 +1293,10 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
       y = ((float)acci * xs) * aux.sc;   // float(acc)*sx*sw
     }
     if (g.epi == E_RESID && !io.resolve1(aux.res, g.res, g.res_st, min(myrow, g.rows - 1), aux.a0)) return false;
-    gemv_epilogue<R>(g, a.out_st, lane, myrow, y, acci, aux, io);
+    gemv_epilogue<R>(g, out_st, lane, myrow, y, acci, aux, io);
     if (b == b0) io.mark(6);   // trace: first batch stored
     si = sin;
+    g = gn;
     aux = auxn;
   }
   return true;
@@ -1373,7 +1458,7 @@ __device__ __forceinline__ bool deltanet_gates(const DnArgs& a, int h, int tokv,
 #pragma unroll
     for (int e = 0; e < 16; ++e) xv[e] = t1[0][e];
   }
-  if (a.gx_norm != nullptr) {   // norm.hpp:13-20, in the GEMV prologue's order (x g) * inv
+  if (a.gx_norm != nullptr) {   // norm.hpp:13-20, in the GEMV prologue's order for the mode
     float nw[16];
     if (a.lanes)
       load16c(a.gx_norm, lane, nw);
@@ -1382,8 +1467,13 @@ __device__ __forceinline__ bool deltanet_gates(const DnArgs& a, int h, int tokv,
     float ss = dot16_f32(xv, xv, 0.0f);
     ss = xor_sum<64>(ss);
     const float inv = 1.0f / sqrtf(ss / 1024.0f + a.eps);
+    if (a.mode == M_W8A8) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) xv[e] = (xv[e] * (1.0f + nw[e])) * inv;
+      for (int e = 0; e < 16; ++e) xv[e] = (xv[e] * (1.0f + nw[e])) * inv;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) xv[e] = (xv[e] * inv) * (1.0f + nw[e]);
+    }
   }
   if (a.mode == M_W8A8) {   // _qa (golden/model.py:37-45), dequantised
     float am = 0.0f;

@@ -56,10 +56,8 @@ MANIFEST_CONFIG_KEYS = ("hidden_size", "num_hidden_layers", "layer_types", "head
 _NP_DTYPES = {"F32": np.float32, "F16": np.float16, "I64": np.int64, "I32": np.int32}
 
 
-def should_quant(name: str, exclude_embed: bool = False) -> bool:
-    """golden/quant.py:36-39."""
-    if exclude_embed and name == "embed_tokens.weight":
-        return False
+def should_quant(name: str) -> bool:
+    """A 2-D tensor with one of these suffixes is stored as per-row int8 (golden/quant.py:36-39)."""
     return any(name.endswith(s) for s in QUANT_SUFFIXES)
 
 
