@@ -81,6 +81,7 @@ struct qh_engine {
   unsigned poll_limit = 1u << 20;  // failed polls before a hand-over wait gives up (QH_POLL_LIMIT)
   bool broken = false;             // a launch returned QH_EDEVICE: decode refused until reset
   int fallbacks = 0;               // cooperative launches refused (each switched the engine to the graph path)
+  bool dn_lds = false;             // the persistent kernel keeps the DeltaNet state in LDS (enough workgroups)
 };
 
 namespace {
@@ -226,6 +227,9 @@ void build_layers(const qh_engine* e, int l0, int l1, bool embed, Bufs& B, std::
       d.o = B.take(kLH * kLV, e->o);
       d.o_st = sB;
       d.gates_in_convd = tag ? 1 : 0;
+      // persistent kernel: this layer's 64 units keep their state in LDS, on workgroups
+      // (64 li + u) % grid, slot (64 li + u) / grid (dn_tiles)
+      d.unit_base = tag && e->dn_lds ? li * kLH * kDnVQuarters : -1;
       d.done = done;
       Stage sd;
       sd.kind = ST_DELTANET;
@@ -507,6 +511,7 @@ int run_persist(qh_engine* e, int tok0, int n_prompt, int n_new, int eos, bool w
   a.logits = with_logits ? e->logits : nullptr;
   a.abort_flag = e->abort_dev;
   a.poll_limit = e->poll_limit;
+  a.dn_lds = e->dn_lds ? 1 : 0;
   QH_HIP(hipEventRecord(e->launch_ev[0], s));
   if (const hipError_t le = launch_persist(a, e->persist_grid, s); le != hipSuccess) {
     (void)hipGetLastError();
@@ -713,6 +718,9 @@ int create(const void* blob, size_t blob_len, const char* idx_text, int max_ctx,
   QH_C(dalloc(&e->part_idx, e->head_grid > 256 ? e->head_grid : 256));
   QH_C(dalloc(&e->abort_dev, 1));
   if (persist_max_grid(&e->persist_grid) != 0) e->persist_grid = 0;
+  // every workgroup holds at most kDnSlots DeltaNet state tiles, one unit per stage
+  e->dn_lds = e->persist_grid >= kLH * kDnVQuarters &&
+              e->persist_grid * kDnSlots >= kNLinear * kLH * kDnVQuarters;
   if (e->persist_grid == 0) e->exec = QH_EXEC_GRAPH;
   QH_C(hip_status(hipEventCreate(&e->launch_ev[0])));
   QH_C(hip_status(hipEventCreate(&e->launch_ev[1])));

@@ -9,6 +9,7 @@ namespace qh {
 constexpr int kRowsPerBatch = 8;     // rows one wave reduces together (LM head, large GEMVs)
 constexpr int kAttnSplit = 16;       // positions per attention split
 constexpr int kDnVQuarters = 4;      // DeltaNet workgroups per head (32 v columns each)
+constexpr int kDnSlots = 5;          // persistent kernel: DeltaNet state tiles per workgroup (LDS)
 
 enum SegKind : int { SEG_I8 = 0, SEG_F32 = 1, SEG_PAIR = 2 };
 enum Epi : int {
@@ -162,6 +163,8 @@ struct DnArgs {
   const int* done = nullptr;
   int convd_st = 0, gx_st = 0;   // producers of convd / gx (tagged I/O)
   int o_st = 0;                  // this stage
+  int unit_base = -1;            // persistent kernel: >= 0 keeps S in LDS for the launch
+                                 // (the layer's global unit index base; see dn_tiles)
 };
 
 struct Floats64 { float v[64]; };
@@ -208,6 +211,7 @@ struct PersistArgs {
   unsigned poll_limit = 1u << 20;   // failed polls before a wait gives up (about a second)
   uint64_t* trace = nullptr;    // optional [trace_tokens][nstage][grid][kTraceSlots]: stage marks and end
   int trace_tokens = 0;
+  int dn_lds = 0;               // DeltaNet stages keep S in LDS (their unit_base >= 0)
 };
 constexpr int kPersistThreads = 256;
 constexpr int kTraceSlots = 8;  // marks 0..6 of a stage body, then its completion time

@@ -55,6 +55,7 @@ __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistA
   const int n_prompt = P.ctl->n_prompt, n_new = P.ctl->n_new, eos = P.ctl->eos, max_ctx = P.ctl->max_ctx;
   int argmax = P.ctl->argmax, done = 0, err = 0, aborted = 0;
   const HeadArgs& hd = P.prog[P.nstage - 1].hd;
+  if (P.dn_lds) dn_tiles_copy(P.prog, P.nstage, blk, nblk, true);   // this workgroup's DeltaNet state tiles
 
   const uint32_t* progw = reinterpret_cast<const uint32_t*>(P.prog);
   uint32_t nxt = t < kStageWords ? progw[t] : 0u;   // descriptor word of stage 0
@@ -139,6 +140,7 @@ __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistA
     }
     if (done) break;
   }
+  if (P.dn_lds) dn_tiles_copy(P.prog, P.nstage, blk, nblk, false);   // the state back to its buffer
   if (blk == 0 && t == 0) {
     StepCtl* c = P.ctl;
     c->tok = tok;

@@ -62,9 +62,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_n(const void* base, int n
 // two per stage, and each copy ends with a workgroup barrier, so a slot is
 // rewritten only after every wave has passed two later barriers -- long after
 // its last read of the slot's previous contents.
+// The per-stage kernels take slots of 4096 floats (op-level K up to 4096); the
+// persistent kernel, whose largest staged vector is the 3584-element MLP
+// activation, takes slots of 3584 so that the DeltaNet state tiles it keeps in
+// LDS fit beside them.  Each kernel allocates only the ring it uses.
 constexpr int kLdsSlot = 4096;
+constexpr int kTagSlot = 3584;
+template <int SLOT>
 __device__ __forceinline__ float* lds_ring() {
-  __shared__ float ring[4 * kLdsSlot];
+  __shared__ float ring[4 * SLOT];
   return ring;
 }
 
@@ -80,7 +86,7 @@ struct PlainIO {
   const int* done = nullptr;   // engine stop flag (graph engine); null: never stopped
   int ring = 0;                // next LDS slot
   int dv = 0;                  // the stop flag, loaded by arrive()
-  __device__ __forceinline__ float* slot() { return lds_ring() + kLdsSlot * (ring++ & 3); }
+  __device__ __forceinline__ float* slot() { return lds_ring<kLdsSlot>() + kLdsSlot * (ring++ & 3); }
   __device__ __forceinline__ void mark(int) {}
   // Issued before any weight load of the stage: a wave's loads return in
   // issue order, so waiting for the flag in wait() then waits for this load
@@ -261,7 +267,7 @@ struct TagIO {
   unsigned poll_limit = kPollLimit;
   bool failed = false;        // this wave gave up a wait (sticky for the launch)
   int ring = 0;               // next LDS slot
-  __device__ __forceinline__ float* slot() { return lds_ring() + kLdsSlot * (ring++ & 3); }
+  __device__ __forceinline__ float* slot() { return lds_ring<kTagSlot>() + kTagSlot * (ring++ & 3); }
   uint64_t* tr = nullptr;     // optional timing trace of the current stage (points 0..2)
   __device__ __forceinline__ void mark(int p) {
     if (tr != nullptr && threadIdx.x == 0) tr[p] = __builtin_amdgcn_s_memrealtime();
@@ -554,7 +560,7 @@ struct TagIO {
     return stage_finish(base, st, K, lds, vp);
   }
   // The whole workgroup (kPersistThreads threads) copies elements [0, K) of a
-  // tagged vector into lds as fp32, K <= 4096 and even: each thread checks the
+  // tagged vector into lds as fp32, K <= kTagSlot and even: each thread checks the
   // tags of its pairs (first loads issued by stage_issue); after a miss every
   // wave polls 64 samples spread over the vector before loading its pairs
   // again.  Ends with a barrier.
@@ -1503,8 +1509,42 @@ __device__ __forceinline__ bool deltanet_gates(const DnArgs& a, int h, int tokv,
 // GATES: g and beta are pairs 6144 + 16 h and 6144 + 16 h + 1 of the tagged
 // convd vector (written by the in_proj stage, see GemvArgs::gw) and arrive
 // with q, k and v; otherwise every wave computes them.
-template <bool GATES, class IO>
-__device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool valid, IO& io, int tokv) {
+// LDS-resident state (persistent kernel): a unit's 128 x 32 slice of S lives in
+// one LDS tile of its workgroup for the whole launch -- thread t's 16 values
+// (rows 16 kg .. 16 kg + 15 of its column) as four quads at (q * 256 + t) * 4,
+// so each of the four 16-byte reads and writes of a wave is one conflict-free
+// 1 KiB span.  The launch loads the tiles from the state buffer at its start
+// and writes them back at its end (persist_kernel); a token reads and writes
+// only LDS.  Unit u of the stage with DnArgs::unit_base b runs on workgroup
+// (b + u) % nblk and keeps its tile in slot (b + u) / nblk: the 18 layers' 1152
+// units spread over all workgroups, kDnSlots tiles at most each.
+constexpr int kDnTile = 128 * 32;   // floats
+__device__ __forceinline__ float* dn_tiles() {
+  __shared__ __attribute__((aligned(16))) float t[kDnSlots * kDnTile];
+  return t;
+}
+__device__ __forceinline__ void dn_tile_read(const float* tile, float* s) {
+  const __attribute__((address_space(3))) f32x4* q = as_lds(reinterpret_cast<const f32x4*>(tile));
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const f32x4 t = q[k * kPersistThreads + threadIdx.x];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s[4 * k + e] = t[e];
+  }
+}
+__device__ __forceinline__ void dn_tile_write(float* tile, const float* s) {
+  __attribute__((address_space(3))) f32x4* q = (__attribute__((address_space(3))) f32x4*)tile;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) q[k * kPersistThreads + threadIdx.x] = f32x4{s[4 * k], s[4 * k + 1], s[4 * k + 2], s[4 * k + 3]};
+}
+// This thread's column and rows of unit u (see deltanet_body).
+__device__ __forceinline__ int dn_col(int unit) {
+  return (unit % kDnVQuarters) * 32 + 8 * (int)(threadIdx.x >> 6) + (int)((threadIdx.x & 63) >> 3);
+}
+
+template <bool GATES, bool LDSS, class IO>
+__device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool valid, IO& io, int tokv,
+                                              float* tile = nullptr) {
   const int h = unit / kDnVQuarters, vq = unit % kDnVQuarters;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kg = lane & 7, v = vq * 32 + 8 * wave + (lane >> 3);
@@ -1526,8 +1566,12 @@ __device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool va
   float g = 0.0f, beta = 0.0f;
   if (valid) {
     io.template pollr_issue<2, M>(a.convd, reg, iv, P);
+    if constexpr (LDSS) {
+      dn_tile_read(tile, s);
+    } else {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = as_global(Sh)[(kg * 16 + i) * 128 + v];
+      for (int i = 0; i < 16; ++i) s[i] = as_global(Sh)[(kg * 16 + i) * 128 + v];
+    }
     // inputs final before in_proj: computed while the hand-over is in flight
     if (!GATES && a.wa != nullptr && !deltanet_gates(a, h, tokv, g, beta, io)) return false;
   }
@@ -1577,10 +1621,11 @@ __device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool va
   for (int i = 0; i < 16; ++i) {   // sweep B: reads the updated S
     s[i] = s[i] + qk[1][i] * d;
     p = p + s[i] * qk[0][i];
-    as_global_w(Sh)[(kg * 16 + i) * 128 + v] = s[i];
+    if constexpr (!LDSS) as_global_w(Sh)[(kg * 16 + i) * 128 + v] = s[i];
   }
   p = xor_sum<8>(p);
   if (kg == 0) io.st1(a.o, a.o_st, h * 128 + v, p);
+  if constexpr (LDSS) dn_tile_write(tile, s);
   return true;
 }
 
@@ -1589,16 +1634,53 @@ __device__ __forceinline__ bool deltanet_body(const DnArgs& a, int unit, bool va
 template <class IO>
 __device__ __forceinline__ bool deltanet_all(const DnArgs& a, int blk, int nblk, IO& io, int tokv) {
   const int units = a.heads * kDnVQuarters;
+  if constexpr (IO::kTagged) {
+    const int ub = __builtin_amdgcn_readfirstlane(a.unit_base);
+    if (ub >= 0) {   // LDS-resident state: one unit per workgroup (nblk >= units, host-checked)
+      const int u = ((blk - ub) % nblk + nblk) % nblk;
+      const bool valid = u < units;
+      float* tile = dn_tiles() + kDnTile * ((ub + (valid ? u : 0)) / nblk);
+      return deltanet_body<true, true>(a, valid ? u : 0, valid, io, tokv, tile);
+    }
+  }
   if (IO::kTagged && a.gates_in_convd) {
-    if (!deltanet_body<true>(a, blk, blk < units, io, tokv)) return false;
+    if (!deltanet_body<true, false>(a, blk, blk < units, io, tokv)) return false;
     for (int u = blk + nblk; u < units; u += nblk)
-      if (!deltanet_body<true>(a, u, true, io, tokv)) return false;
+      if (!deltanet_body<true, false>(a, u, true, io, tokv)) return false;
   } else {
-    if (!deltanet_body<false>(a, blk, blk < units, io, tokv)) return false;
+    if (!deltanet_body<false, false>(a, blk, blk < units, io, tokv)) return false;
     for (int u = blk + nblk; u < units; u += nblk)
-      if (!deltanet_body<false>(a, u, true, io, tokv)) return false;
+      if (!deltanet_body<false, false>(a, u, true, io, tokv)) return false;
   }
   return true;
+}
+
+// The LDS tiles of workgroup blk: every DeltaNet stage of the program with a
+// unit on this workgroup copies its slice of S between the state buffer and
+// LDS (to_lds: at the launch start; otherwise back, at its end).
+__device__ __forceinline__ void dn_tiles_copy(const Stage* prog, int nstage, int blk, int nblk, bool to_lds) {
+  const int t = threadIdx.x, kg = (t & 63) & 7;
+  for (int i = 0; i < nstage; ++i) {
+    if (prog[i].kind != ST_DELTANET) continue;
+    const int ub = prog[i].d.unit_base;
+    if (ub < 0) continue;
+    const int units = prog[i].d.heads * kDnVQuarters;
+    const int u = ((blk - ub) % nblk + nblk) % nblk;
+    if (u >= units) continue;
+    float* tile = dn_tiles() + kDnTile * ((ub + u) / nblk);
+    float* Sh = prog[i].d.S + (size_t)(u / kDnVQuarters) * 128 * 128;
+    const int v = dn_col(u);
+    float s[16];
+    if (to_lds) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) s[k] = Sh[(kg * 16 + k) * 128 + v];
+      dn_tile_write(tile, s);
+    } else {
+      dn_tile_read(tile, s);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) Sh[(kg * 16 + k) * 128 + v] = s[k];
+    }
+  }
 }
 
 // ===========================================================================
