@@ -282,7 +282,7 @@ void build_layers(const qh_engine* e, int l0, int l1, bool embed, Bufs& B, std::
       a.seg[2] = mkseg(SEG_I8, E_STORE, kKVProj, a.seg[1].batch0 + a.seg[1].nbatch, B.at(qkv, kQProj + kKVProj));
       a.seg[2].w = i8p(e, l, R_VP);
       a.seg[2].sw = scp(e, l, R_VP);
-      out.push_back(gemv_stage(ST_GEMV_NORM_1x8, a));
+      out.push_back(gemv_stage(ST_GEMV_QKV_1x8, a));
       const int sB = (int)out.size();
       AttnArgs at;
       at.qkv = qkv;
@@ -349,7 +349,7 @@ void build_layers(const qh_engine* e, int l0, int l1, bool embed, Bufs& B, std::
     m.seg[0].sw = scp(e, l, R_GATE);
     m.seg[0].w2 = i8p(e, l, R_UP);
     m.seg[0].sw2 = scp(e, l, R_UP);
-    out.push_back(gemv_stage(ST_GEMV_NORM_1x8, m));
+    out.push_back(gemv_stage(ST_GEMV_GATEUP_1x8, m));
     const int sE = (int)out.size();
     GemvArgs dn;
     dn.K = kInter;
@@ -399,6 +399,8 @@ int launch_stages(qh_engine* e, const std::vector<Stage>& v, hipStream_t s, hipE
   for (const Stage& st : v) {
     switch (st.kind) {
       case ST_GEMV_NORM_1x8:
+      case ST_GEMV_QKV_1x8:
+      case ST_GEMV_GATEUP_1x8:
       case ST_GEMV_GATED_2x1:
       case ST_GEMV_LOAD_2x1:
       case ST_GEMV_LOAD_4x1: QH_HIP(launch_gemv(st.g, 4, s)); break;
@@ -446,14 +448,24 @@ int ensure_prog(qh_engine* e) {
   build_layers(e, 0, kLayers, true, B, v, h);
   v.push_back(head_stage(e, B, h, false, (int)v.size(), e->persist_grid));
   if ((int)v.size() >= kTagsPerToken || B.used != e->arena_pairs) return QH_ESTATE;
-  // the persistent kernel compiles each GEMV stage kind for one vector length
+  // the persistent kernel compiles each GEMV stage kind for one vector length and one set of
+  // epilogues and segment kinds
   for (const Stage& st : v) {
-    const int want = st.kind == ST_GEMV_NORM_1x8    ? kHidden
+    const int want = (st.kind == ST_GEMV_NORM_1x8 || st.kind == ST_GEMV_QKV_1x8 || st.kind == ST_GEMV_GATEUP_1x8)
+                         ? kHidden
                      : st.kind == ST_GEMV_GATED_2x1 ? kLH * kLV
                      : st.kind == ST_GEMV_LOAD_2x1  ? kNH * kHD
                      : st.kind == ST_GEMV_LOAD_4x1  ? kInter
                                                     : -1;
-    if (want >= 0 && st.g.K != want) return QH_ESTATE;
+    if (want < 0) continue;
+    if (st.g.K != want) return QH_ESTATE;
+    const int em = stage_em(st.kind);
+    for (int i = 0; i < st.g.nseg; ++i) {
+      const Seg& g = st.g.seg[i];
+      if (!(em & (1 << g.epi))) return QH_ESTATE;
+      if (g.kind == SEG_PAIR && !(em & kEmPair)) return QH_ESTATE;
+      if (g.kind == SEG_F32 && !(em & kEmF32)) return QH_ESTATE;
+    }
   }
   QH_TRY(dalloc(&e->prog[e->mode], v.size()));
   QH_HIP(hipMemcpy(e->prog[e->mode], v.data(), sizeof(Stage) * v.size(), hipMemcpyHostToDevice));

@@ -173,7 +173,7 @@ struct Floats64 { float v[64]; };
 // which body runs them.  The three K > 1024 GEMVs use one row per wave batch
 // (1024 rows = 1024 batches), so every wave of a 256-workgroup grid streams.
 enum StageKind : int {
-  ST_GEMV_NORM_1x8 = 0,    // gemv_body<1, mode, P_NORM, 8>   in_proj / q,k,v / gate,up
+  ST_GEMV_NORM_1x8 = 0,    // gemv_body<1, mode, P_NORM, 8>   DeltaNet in_proj (conv + SiLU, SiLU(z), gate rows)
   ST_GEMV_GATED_2x1 = 1,   // gemv_body<2, mode, P_GATED, 1>  DeltaNet out_proj
   ST_GEMV_LOAD_2x1 = 2,    // gemv_body<2, mode, P_LOAD, 1>   attention o_proj
   ST_GEMV_LOAD_4x1 = 3,    // gemv_body<4, mode, P_LOAD, 1>   MLP down
@@ -181,7 +181,26 @@ enum StageKind : int {
   ST_ATTN = 5,
   ST_COMBINE = 6,
   ST_HEAD = 7,
+  ST_GEMV_QKV_1x8 = 8,     // gemv_body<1, mode, P_NORM, 8>   attention q||gate, k, v (E_STORE only)
+  ST_GEMV_GATEUP_1x8 = 9,  // gemv_body<1, mode, P_NORM, 8>   MLP gate||up pairs (E_SWIGLU only)
 };
+// The epilogues (and segment kinds) a GEMV stage kind may hold, as a mask of
+// (1 << Epi) bits plus kEmPair / kEmF32; 0 allows everything.  The persistent
+// kernel compiles each stage kind for its own set, so loads and branches for
+// the others do not exist there; the engine checks its program against them.
+constexpr int kEmPair = 1 << 14;   // SEG_PAIR segments
+constexpr int kEmF32 = 1 << 13;    // SEG_F32 segments
+constexpr int kEmInProj = (1 << E_CONV) | (1 << E_SILU);   // ST_GEMV_NORM_1x8 (DeltaNet in_proj)
+constexpr int kEmStore = 1 << E_STORE;                     // ST_GEMV_QKV_1x8
+constexpr int kEmSwiglu = (1 << E_SWIGLU) | kEmPair;       // ST_GEMV_GATEUP_1x8
+constexpr int kEmResid = 1 << E_RESID;                     // the 2x1 / 4x1 kinds
+constexpr int stage_em(int kind) {
+  return kind == ST_GEMV_NORM_1x8     ? kEmInProj
+         : kind == ST_GEMV_QKV_1x8    ? kEmStore
+         : kind == ST_GEMV_GATEUP_1x8 ? kEmSwiglu
+         : (kind == ST_GEMV_GATED_2x1 || kind == ST_GEMV_LOAD_2x1 || kind == ST_GEMV_LOAD_4x1) ? kEmResid
+                                      : 0;
+}
 struct Stage {
   int kind = ST_GEMV_NORM_1x8;
   union {   // the arguments of `kind` (all members are trivially copyable)

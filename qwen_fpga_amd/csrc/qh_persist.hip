@@ -79,11 +79,15 @@ __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistA
       io.tr = tr;
       bool ok;
       switch (st.kind) {
-        // the vector lengths of the stage kinds are fixed (the engine checks its program)
-        case ST_GEMV_NORM_1x8: ok = gemv_body<1, MODE, P_NORM, 8, QH_HIDDEN>(st.g, blk, nblk, io, tok); break;
-        case ST_GEMV_GATED_2x1: ok = gemv_body<2, MODE, P_GATED, 1, QH_LH * QH_LV>(st.g, blk, nblk, io, tok); break;
-        case ST_GEMV_LOAD_2x1: ok = gemv_body<2, MODE, P_LOAD, 1, QH_NH * QH_HD>(st.g, blk, nblk, io, tok); break;
-        case ST_GEMV_LOAD_4x1: ok = gemv_body<4, MODE, P_LOAD, 1, QH_INTER>(st.g, blk, nblk, io, tok); break;
+        // the vector length and epilogues of each GEMV stage kind are fixed (the engine checks its program)
+        case ST_GEMV_NORM_1x8: ok = gemv_body<1, MODE, P_NORM, 8, QH_HIDDEN, kEmInProj>(st.g, blk, nblk, io, tok); break;
+        case ST_GEMV_QKV_1x8: ok = gemv_body<1, MODE, P_NORM, 8, QH_HIDDEN, kEmStore>(st.g, blk, nblk, io, tok); break;
+        case ST_GEMV_GATEUP_1x8:
+          ok = gemv_body<1, MODE, P_NORM, 8, QH_HIDDEN, kEmSwiglu>(st.g, blk, nblk, io, tok);
+          break;
+        case ST_GEMV_GATED_2x1: ok = gemv_body<2, MODE, P_GATED, 1, QH_LH * QH_LV, kEmResid>(st.g, blk, nblk, io, tok); break;
+        case ST_GEMV_LOAD_2x1: ok = gemv_body<2, MODE, P_LOAD, 1, QH_NH * QH_HD, kEmResid>(st.g, blk, nblk, io, tok); break;
+        case ST_GEMV_LOAD_4x1: ok = gemv_body<4, MODE, P_LOAD, 1, QH_INTER, kEmResid>(st.g, blk, nblk, io, tok); break;
         case ST_DELTANET: ok = deltanet_all(st.d, blk, nblk, io, tok); break;
         case ST_ATTN: ok = attn_body(st.at, pos, blk, nblk, io); break;
         case ST_COMBINE: ok = combine_body(st.at, pos, blk, io); break;

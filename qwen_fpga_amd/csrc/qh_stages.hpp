@@ -766,6 +766,12 @@ __device__ __forceinline__ float i8_at(const uint32_t* w, int e) {
   return (float)(int)(int8_t)(w[e >> 2] >> (8 * (e & 3)));
 }
 
+// Whether epilogue / segment-kind bit `bit` is possible in a GEMV compiled for mask EM.
+template <int EM>
+__device__ __forceinline__ constexpr bool em_has(int bit) {
+  return EM == 0 || (EM & bit) != 0;
+}
+
 // Per-row epilogue inputs, loaded by every lane for its row at batch start.
 struct EpiAux {
   float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;   // residual | conv state cols 1..3 | A_log
@@ -777,40 +783,48 @@ struct EpiAux {
 // segment's epilogue does not use come from zero-size descriptors (no memory
 // access), so the load block stays straight-line and the compiler can count
 // outstanding loads exactly.
-template <class IO>
+template <int EM, class IO>
 __device__ __forceinline__ void epi_prefetch(const Seg& g, int myrow, EpiAux& x, IO& io) {
   constexpr int kBig = 0x7ffffff0;
   const int r = min(myrow, g.rows - 1);   // always a valid address; unused rows are never stored
-  const bool pair = g.kind == SEG_PAIR;
+  const bool pair = em_has<EM>(kEmPair) && g.kind == SEG_PAIR;
+  const bool f32 = em_has<EM>(kEmF32) && g.kind == SEG_F32;
   // the row's scale: lanes of a pair segment take even rows (gate) from sw and
   // odd rows (up) from sw2, so both are loaded through uniform descriptors
-  const int i8n = (g.kind == SEG_F32 || g.sw == nullptr) ? 0 : kBig;   // no scales: E_ACCI
+  const int i8n = (f32 || g.sw == nullptr) ? 0 : kBig;   // no scales: E_ACCI
   const int si = (pair ? (r >> 1) : r) * 4;
   const float sa = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_n(g.sw, i8n), si, 0, 0));
-  const float sb = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_n(g.sw2, pair ? kBig : 0), si, 0, 0));
-  x.sc = g.kind == SEG_F32 ? 1.0f : ((pair && (r & 1)) ? sb : sa);
-  x.res = io.issue1(g.res, r, g.epi == E_RESID);   // residual: written by another workgroup
-  const bool ga = g.epi == E_GATE_A, cv = g.epi == E_CONV;
-  const float a_log = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_n(g.c0, ga ? kBig : 0), r * 4, 0, 0));
-  const float dtb = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_n(g.c1, ga ? kBig : 0), r * 4, 0, 0));
-  const u32x4 st = __builtin_amdgcn_raw_buffer_load_b128(rsrc_n(g.c2, cv ? kBig : 0), r * 16, 0, 0);
-  const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rsrc_n(g.c0, cv ? kBig : 0), r * 16, 0, 0);
-  x.a0 = a_log;   // E_GATE_A: A_log (E_RESID overwrites a0 once the residual resolves)
-  x.w0 = ga ? dtb : __uint_as_float(w[0]);
-  x.a1 = __uint_as_float(st[1]);
-  x.a2 = __uint_as_float(st[2]);
-  x.a3 = __uint_as_float(st[3]);
-  x.w1 = __uint_as_float(w[1]);
-  x.w2 = __uint_as_float(w[2]);
-  x.w3 = __uint_as_float(w[3]);
+  float sb = 0.0f;
+  if constexpr (em_has<EM>(kEmPair))
+    sb = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_n(g.sw2, pair ? kBig : 0), si, 0, 0));
+  x.sc = f32 ? 1.0f : ((pair && (r & 1)) ? sb : sa);
+  if constexpr (em_has<EM>(1 << E_RESID))
+    x.res = io.issue1(g.res, r, g.epi == E_RESID);   // residual: written by another workgroup
+  if constexpr (em_has<EM>(1 << E_GATE_A)) {
+    const bool ga = g.epi == E_GATE_A;
+    x.a0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_n(g.c0, ga ? kBig : 0), r * 4, 0, 0));
+    x.w0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_n(g.c1, ga ? kBig : 0), r * 4, 0, 0));
+  }
+  if constexpr (em_has<EM>(1 << E_CONV)) {
+    const bool cv = g.epi == E_CONV;
+    const u32x4 st = __builtin_amdgcn_raw_buffer_load_b128(rsrc_n(g.c2, cv ? kBig : 0), r * 16, 0, 0);
+    const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rsrc_n(g.c0, cv ? kBig : 0), r * 16, 0, 0);
+    if (cv) x.w0 = __uint_as_float(w[0]);   // (E_GATE_A keeps dt_bias in w0)
+    x.a1 = __uint_as_float(st[1]);
+    x.a2 = __uint_as_float(st[2]);
+    x.a3 = __uint_as_float(st[3]);
+    x.w1 = __uint_as_float(w[1]);
+    x.w2 = __uint_as_float(w[2]);
+    x.w3 = __uint_as_float(w[3]);
+  }
 }
 
 // Row-batch epilogue: the writer lane of each row stores its result y.
-template <int R, class IO>
+template <int R, int EM, class IO>
 __device__ __forceinline__ void gemv_epilogue(const Seg& g, int ost, int lane, int myrow, float y, int acci,
                                               const EpiAux& x, IO& io) {
   constexpr int LPR = 64 / R;   // lanes holding one row
-  if constexpr (R >= 2) {
+  if constexpr (R >= 2 && em_has<EM>(1 << E_SWIGLU)) {
     if (g.epi == E_SWIGLU) {      // pair rows: even = gate i, odd = up i (mlp.hpp:17)
       const float yo = xperm<LPR>(y);
       if ((lane & (2 * LPR - 1)) == 0 && myrow < g.rows) io.st1(g.out, ost, myrow >> 1, dev_silu(y) * yo);
@@ -818,41 +832,38 @@ __device__ __forceinline__ void gemv_epilogue(const Seg& g, int ost, int lane, i
     }
   }
   if ((lane & (LPR - 1)) != 0 || myrow >= g.rows) return;
-  switch (g.epi) {
-    case E_STORE:
-      io.st1(g.out, ost, myrow, y);
-      break;
-    case E_SILU:   // silu(z) for the gated norm (norm.hpp:32)
-      io.st1(g.out, ost, myrow, dev_silu(y));
-      break;
-    case E_RESID:
-      io.st1(g.out, ost, myrow, x.a0 + y);
-      break;
-    case E_ACC:
-      io.st1(g.out, ost, myrow, y);
-      as_global_w(g.acc_out)[myrow] = acci;
-      break;
-    case E_ACCI:
-      as_global_w(g.acc_out)[myrow] = acci;
-      break;
-    case E_GATE_B:
-      io.st1(g.out, ost, myrow, dev_sigmoid(y));
-      break;
-    case E_GATE_A:
-      io.st1(g.out, ost, myrow, -dev_expf(x.a0) * dev_softplus(y + x.w0));
-      break;
-    case E_CONV: {   // conv1d.hpp:22-36: window = state cols 1..3 + new sample
-      float acc = 0.0f;
-      acc = acc + x.a1 * x.w0;
-      acc = acc + x.a2 * x.w1;
-      acc = acc + x.a3 * x.w2;
-      acc = acc + y * x.w3;
-      *as_global_w(reinterpret_cast<f32x4*>(g.c2 + (size_t)myrow * 4)) = f32x4{x.a1, x.a2, x.a3, y};
-      io.st1(g.out, ost, myrow, dev_silu(acc));
-      break;
-    }
-    default:
-      break;
+  if constexpr (EM == kEmResid) {   // the only epilogue of the 2x1 / 4x1 kinds
+    io.st1(g.out, ost, myrow, x.a0 + y);
+    return;
+  }
+  if constexpr (EM == kEmStore) {
+    io.st1(g.out, ost, myrow, y);
+    return;
+  }
+  const int epi = g.epi;
+  if (em_has<EM>(1 << E_STORE) && epi == E_STORE) {
+    io.st1(g.out, ost, myrow, y);
+  } else if (em_has<EM>(1 << E_SILU) && epi == E_SILU) {   // silu(z) for the gated norm (norm.hpp:32)
+    io.st1(g.out, ost, myrow, dev_silu(y));
+  } else if (em_has<EM>(1 << E_RESID) && epi == E_RESID) {
+    io.st1(g.out, ost, myrow, x.a0 + y);
+  } else if (em_has<EM>(1 << E_ACC) && epi == E_ACC) {
+    io.st1(g.out, ost, myrow, y);
+    as_global_w(g.acc_out)[myrow] = acci;
+  } else if (em_has<EM>(1 << E_ACCI) && epi == E_ACCI) {
+    as_global_w(g.acc_out)[myrow] = acci;
+  } else if (em_has<EM>(1 << E_GATE_B) && epi == E_GATE_B) {
+    io.st1(g.out, ost, myrow, dev_sigmoid(y));
+  } else if (em_has<EM>(1 << E_GATE_A) && epi == E_GATE_A) {
+    io.st1(g.out, ost, myrow, -dev_expf(x.a0) * dev_softplus(y + x.w0));
+  } else if (em_has<EM>(1 << E_CONV) && epi == E_CONV) {   // conv1d.hpp:22-36: window = state cols 1..3 + new
+    float acc = 0.0f;
+    acc = acc + x.a1 * x.w0;
+    acc = acc + x.a2 * x.w1;
+    acc = acc + x.a3 * x.w2;
+    acc = acc + y * x.w3;
+    *as_global_w(reinterpret_cast<f32x4*>(g.c2 + (size_t)myrow * 4)) = f32x4{x.a1, x.a2, x.a3, y};
+    io.st1(g.out, ost, myrow, dev_silu(acc));
   }
 }
 
@@ -888,11 +899,11 @@ __device__ __forceinline__ Seg seg_uniform(const Seg& s) {
 // int8 rows: its descriptors are empty and the loads read nothing.  g and row0
 // are wave-uniform: a row's byte offset goes in the scalar offset of the
 // buffer load, and only the lane's chunk offset is per lane.
-template <int NCH, int R>
+template <int NCH, int R, int EM>
 __device__ __forceinline__ void load_batch(const Seg& g, int row0, int K, int nchunk, int lane,
                                            uint32_t (&w)[NCH][R][4]) {
-  const bool pair = g.kind == SEG_PAIR;
-  const int n = g.kind == SEG_F32 ? 0 : 0x7ffffff0;
+  const bool pair = em_has<EM>(kEmPair) && g.kind == SEG_PAIR;
+  const int n = (em_has<EM>(kEmF32) && g.kind == SEG_F32) ? 0 : 0x7ffffff0;
   const int last = g.rows - 1;
   const __amdgpu_buffer_rsrc_t rw = rsrc_n(g.w, n);
   const __amdgpu_buffer_rsrc_t rw2 = rsrc_n(pair ? g.w2 : g.w, n);
@@ -926,7 +937,7 @@ __device__ __forceinline__ uint32_t* gemv_qlds() {
 
 // KC: the vector length when the caller knows it at compile time (the
 // persistent kernel's stage kinds), 0 to take it from the descriptor.
-template <int NCH, int MODE, int PRO, int R, int KC = 0, class IO>
+template <int NCH, int MODE, int PRO, int R, int KC = 0, int EM = 0, class IO>
 __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, IO& io, int tokv) {
   const int lane = threadIdx.x & 63, nwv = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -968,7 +979,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
   for (int i = 0; i < 4; ++i)
     if (i < nseg) {
       total = sb0[i] + snb[i];   // segments are in batch order: the last one ends the range
-      has_f32 = has_f32 || skind[i] == SEG_F32;
+      has_f32 = has_f32 || (em_has<EM>(kEmF32) && skind[i] == SEG_F32);
     }
   total = __builtin_amdgcn_readfirstlane(total);
   has_f32 = __builtin_amdgcn_readfirstlane((int)has_f32) != 0;
@@ -1030,8 +1041,8 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
   // is issued before them and its wait does not include the weights.
   {
     const int row0 = __builtin_amdgcn_readfirstlane((bq - g.batch0) * R);
-    load_batch<NCH, R>(g, row0, K, nchunk, lane, w);   // SEG_F32: never read
-    epi_prefetch(g, row0 + row_of_lane<R>(lane), aux, io);
+    load_batch<NCH, R, EM>(g, row0, K, nchunk, lane, w);   // SEG_F32: never read
+    epi_prefetch<EM>(g, row0 + row_of_lane<R>(lane), aux, io);
   }
   if (!io.wait()) return false;
   // the workgroup's copy of x (and z): every wave takes part, rows or not
@@ -1237,7 +1248,8 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
     int acci = 0;
     float pf[R];
     int pi[R];
-    if (g.kind == SEG_F32) {   // fp32 weights (gemv.hpp:46-59)
+    const bool f32 = em_has<EM>(kEmF32) && g.kind == SEG_F32;
+    if (f32) {   // fp32 weights (gemv.hpp:46-59)
 #pragma unroll
       for (int r = 0; r < R; ++r) pf[r] = 0.0f;
 #pragma unroll
@@ -1272,7 +1284,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
     }
     if (b == b0) {   // trace: dot products of the first batch done (its weights arrived)
       if constexpr (MODE == M_W8A8) {
-        if (g.kind != SEG_F32) asm volatile("" ::"v"(pi[0]));
+        if (!f32) asm volatile("" ::"v"(pi[0]));
         else asm volatile("" ::"v"(pf[0]));
       } else {
         asm volatile("" ::"v"(pf[0]));
@@ -1288,18 +1300,20 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
       sin = seg_index(bn);
       if (sin != si) gn = seg_uniform(a.seg[sin]);
       const int rn = __builtin_amdgcn_readfirstlane((bn - gn.batch0) * R);
-      if (gn.kind != SEG_F32) load_batch<NCH, R>(gn, rn, K, nchunk, lane, w);
-      epi_prefetch(gn, rn + row_of_lane<R>(lane), auxn, io);
+      if (!(em_has<EM>(kEmF32) && gn.kind == SEG_F32)) load_batch<NCH, R, EM>(gn, rn, K, nchunk, lane, w);
+      epi_prefetch<EM>(gn, rn + row_of_lane<R>(lane), auxn, io);
     }
-    if (g.kind == SEG_F32 || MODE == M_W8A16) {
+    if (f32 || MODE == M_W8A16) {
       y = reduce_rows<R>(pf, lane);
-      if (g.kind != SEG_F32) y = y * aux.sc;
+      if (!f32) y = y * aux.sc;
     } else {
       acci = reduce_rows<R>(pi, lane);
       y = ((float)acci * xs) * aux.sc;   // float(acc)*sx*sw
     }
-    if (g.epi == E_RESID && !io.resolve1(aux.res, g.res, g.res_st, min(myrow, g.rows - 1), aux.a0)) return false;
-    gemv_epilogue<R>(g, out_st, lane, myrow, y, acci, aux, io);
+    if (em_has<EM>(1 << E_RESID) && g.epi == E_RESID &&
+        !io.resolve1(aux.res, g.res, g.res_st, min(myrow, g.rows - 1), aux.a0))
+      return false;
+    gemv_epilogue<R, EM>(g, out_st, lane, myrow, y, acci, aux, io);
     if (b == b0) io.mark(6);   // trace: first batch stored
     si = sin;
     g = gn;
@@ -1325,13 +1339,16 @@ __device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
 // unconditionally: a batch beyond the last one goes through empty descriptors
 // (no memory access, reads 0), so the loop keeps no conditionally loaded
 // registers and the compiler waits for exactly the batch it consumes.
+// hw / hsw: the weight and scale bases, wave-uniform values the caller read
+// from the descriptor once (read through the descriptor here, they would be
+// read from LDS again at every batch: the logits stores may alias it).
 template <int POL>
-__device__ __forceinline__ void head_load(const HeadArgs& a, int b, int total, int lane, int rl, uint32_t (&w)[8][4],
-                                          float& sc) {
+__device__ __forceinline__ void head_load(const int8_t* hw, const float* hsw, int b, int total, int lane, int rl,
+                                          uint32_t (&w)[8][4], float& sc) {
   b = __builtin_amdgcn_readfirstlane(b);   // wave-uniform: scalar descriptors
   const bool in = b < total;
-  const __amdgpu_buffer_rsrc_t rw = rsrc_n(a.w, in ? 0x7ffffff0 : 0);
-  const __amdgpu_buffer_rsrc_t rs = rsrc_n(a.sw, in ? 0x7ffffff0 : 0);
+  const __amdgpu_buffer_rsrc_t rw = rsrc_n(hw, in ? 0x7ffffff0 : 0);
+  const __amdgpu_buffer_rsrc_t rs = rsrc_n(hsw, in ? 0x7ffffff0 : 0);
   const int bb = in ? b : 0;
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
@@ -1348,7 +1365,9 @@ template <class IO>
 __device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, IO& io, float* logits) {
   const int lane = threadIdx.x & 63, nwv = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int total = a.rows / kRowsPerBatch;
+  const int total = __builtin_amdgcn_readfirstlane(a.rows / kRowsPerBatch);
+  const int8_t* const hw = static_cast<const int8_t*>(wave_uniform(a.w));
+  const float* const hsw = static_cast<const float*>(wave_uniform(a.sw));
   const int stride = nblk * nwv;
   int b = blk * nwv + wave;
   const int rl = (lane >> 3) & 7;
@@ -1357,8 +1376,8 @@ __device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, 
   io.stage_issue(a.h, 1024, vh);
   uint32_t w0[8][4], w1[8][4];
   float sc0 = 0.0f, sc1 = 0.0f;
-  head_load<kNt>(a, b, total, lane, rl, w0, sc0);   // two batches in flight before the norm prologue
-  head_load<0>(a, b + stride, total, lane, rl, w1, sc1);
+  head_load<kNt>(hw, hsw, b, total, lane, rl, w0, sc0);   // two batches in flight before the norm prologue
+  head_load<0>(hw, hsw, b + stride, total, lane, rl, w1, sc1);
   float xv[16], nw[16];
   if (a.nw_lanes)
     load16c(a.nw, lane, nw);
@@ -1387,7 +1406,7 @@ __device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, 
     for (int r = 0; r < 8; ++r) p[r] = dot16_i8f(w[r], xv, 0.0f);
     float scur;   // an explicit copy frees sc's register for the next load (no copy at the loop latch)
     asm volatile("v_mov_b32 %0, %1" : "=v"(scur) : "v"(sc));
-    head_load<decltype(pol)::value>(a, bb + 2 * stride, total, lane, rl, w, sc);
+    head_load<decltype(pol)::value>(hw, hsw, bb + 2 * stride, total, lane, rl, w, sc);
     const float y = reduce8(p, lane) * scur;
     const int row = bb * 8 + rl;
     if ((lane & 7) == 0) {
