@@ -279,6 +279,10 @@ template <typename T>
 __device__ __forceinline__ const __attribute__((address_space(3))) T* as_lds(const T* p) {
   return (const __attribute__((address_space(3))) T*)p;
 }
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(3))) T* as_lds_w(T* p) {
+  return (__attribute__((address_space(3))) T*)p;
+}
 
 __device__ __forceinline__ float ldc(const float* p) {
   return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,

@@ -53,12 +53,11 @@ hipError_t launch_gemv(const GemvArgs& a, int waves_per_block, hipStream_t s) {
   const int total = a.seg[a.nseg - 1].batch0 + a.seg[a.nseg - 1].nbatch;
   const int grid = (total + waves_per_block - 1) / waves_per_block;
   const dim3 blk(64 * waves_per_block);
-  if (a.rows_per_batch < 2)
+  if (a.rows_per_batch < 4)
     for (int i = 0; i < a.nseg; ++i)
-      if (a.seg[i].epi == E_SWIGLU) return hipErrorInvalidValue;   // pair rows need R >= 2
+      if (a.seg[i].epi == E_SWIGLU) return hipErrorInvalidValue;   // pair rows need R >= 4
   switch (a.rows_per_batch) {
     case 1: return launch_gemv_r<1>(a, grid, blk, s);
-    case 2: return launch_gemv_r<2>(a, grid, blk, s);
     case 4: return launch_gemv_r<4>(a, grid, blk, s);
     case 8: return launch_gemv_r<8>(a, grid, blk, s);
     default: return hipErrorInvalidValue;

@@ -51,7 +51,7 @@ struct Seg {
 
 struct GemvArgs {
   int K = 0, mode = M_W8A16, prologue = P_LOAD;
-  int rows_per_batch = 8;       // 4 or 8 rows reduced together per wave
+  int rows_per_batch = 8;       // 1, 4 or 8 rows reduced together per wave
   const float* x = nullptr;     // P_LOAD / P_NORM input, P_GATED o
   const float* nw = nullptr;    // P_NORM [K] gain, P_GATED [128] gain
   int nw_lanes = 0;             // P_NORM, K = 1024: nw in the lane-interleaved order (load16c)

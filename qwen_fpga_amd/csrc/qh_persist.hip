@@ -85,9 +85,25 @@ __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistA
         case ST_GEMV_GATEUP_1x8:
           ok = gemv_body<1, MODE, P_NORM, 8, QH_HIDDEN, kEmSwiglu>(st.g, blk, nblk, io, tok);
           break;
-        case ST_GEMV_GATED_2x1: ok = gemv_body<2, MODE, P_GATED, 1, QH_LH * QH_LV, kEmResid>(st.g, blk, nblk, io, tok); break;
-        case ST_GEMV_LOAD_2x1: ok = gemv_body<2, MODE, P_LOAD, 1, QH_NH * QH_HD, kEmResid>(st.g, blk, nblk, io, tok); break;
-        case ST_GEMV_LOAD_4x1: ok = gemv_body<4, MODE, P_LOAD, 1, QH_INTER, kEmResid>(st.g, blk, nblk, io, tok); break;
+        // W8A8 1024-row projections: the vector split over the four waves (same values)
+        case ST_GEMV_GATED_2x1:
+          if (MODE == M_W8A8 && gemv_splitk_ok(st.g, nblk, kPersistThreads / 64))
+            ok = gemv_splitk<2, P_GATED, QH_LH * QH_LV>(st.g, blk, io);
+          else
+            ok = gemv_body<2, MODE, P_GATED, 1, QH_LH * QH_LV, kEmResid>(st.g, blk, nblk, io, tok);
+          break;
+        case ST_GEMV_LOAD_2x1:
+          if (MODE == M_W8A8 && gemv_splitk_ok(st.g, nblk, kPersistThreads / 64))
+            ok = gemv_splitk<2, P_LOAD, QH_NH * QH_HD>(st.g, blk, io);
+          else
+            ok = gemv_body<2, MODE, P_LOAD, 1, QH_NH * QH_HD, kEmResid>(st.g, blk, nblk, io, tok);
+          break;
+        case ST_GEMV_LOAD_4x1:
+          if (MODE == M_W8A8 && gemv_splitk_ok(st.g, nblk, kPersistThreads / 64))
+            ok = gemv_splitk<4, P_LOAD, QH_INTER>(st.g, blk, io);
+          else
+            ok = gemv_body<4, MODE, P_LOAD, 1, QH_INTER, kEmResid>(st.g, blk, nblk, io, tok);
+          break;
         case ST_DELTANET: ok = deltanet_all(st.d, blk, nblk, io, tok); break;
         case ST_ATTN: ok = attn_body(st.at, pos, blk, nblk, io); break;
         case ST_COMBINE: ok = combine_body(st.at, pos, blk, io); break;

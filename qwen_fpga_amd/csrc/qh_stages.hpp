@@ -678,17 +678,6 @@ __device__ __forceinline__ T reduce4(T v[4], int) {
 }
 
 template <typename T>
-__device__ __forceinline__ T reduce2(T v[2], int) {
-  T r = swap_add<32>(v[0], v[1]);
-  r = swap_add<16>(r, r);
-  r = r + xperm<8>(r);
-  r = r + xperm<4>(r);
-  r = r + xperm<2>(r);
-  r = r + xperm<1>(r);
-  return r;
-}
-
-template <typename T>
 __device__ __forceinline__ T reduce1(T v[1], int) {
   T r = swap_add<32>(v[0], v[0]);
   r = swap_add<16>(r, r);
@@ -705,14 +694,17 @@ __device__ __forceinline__ T reduce_rows(T v[R], int lane) {
     return reduce8(v, lane);
   else if constexpr (R == 4)
     return reduce4(v, lane);
-  else if constexpr (R == 2)
-    return reduce2(v, lane);
-  else
+  else {
+    // (two rows go through reduce4 with two zero rows: a two-row tree built on
+    // the permlane swaps gave wrong sums for its second row)
+    static_assert(R == 1, "rows per wave: 1, 4 or 8");
     return reduce1(v, lane);
+  }
 }
 template <int R>
 __device__ __forceinline__ int row_of_lane(int lane) {
-  return R == 1 ? 0 : (lane >> (R == 8 ? 3 : R == 4 ? 4 : 5)) & (R - 1);
+  static_assert(R == 1 || R == 4 || R == 8, "rows per wave: 1, 4 or 8");
+  return R == 1 ? 0 : (lane >> (R == 8 ? 3 : 4)) & (R - 1);
 }
 
 // 16 floats from global memory (load16g) or LDS (load16l), 16-byte aligned
@@ -1319,6 +1311,155 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
     g = gn;
     aux = auxn;
   }
+  return true;
+}
+
+// ===========================================================================
+// W8A8 GEMV with one output row per wave and the vector split over the
+// workgroup's four waves (the 1024-row projections with K = 2048 or 3584:
+// DeltaNet out_proj, attention o_proj, MLP down).  The workgroup owns rows
+// rb .. rb + 3; wave w takes chunk jw = w % NCH of every lane (elements
+// 16 (lane + 64 jw) .. +15) for the NCH rows of group w / NCH, so it stages,
+// normalises and quantises a quarter (NCH = 4) or half (NCH = 2) of the vector
+// instead of all of it.  The maxima of the chunks meet in LDS (max is exact in
+// any order), every wave quantises its chunk with the vector's scale, forms the
+// int32 lane partials of its rows, reduces them over the lanes and leaves them
+// in LDS; wave w then adds the NCH partials of row rb + w (int32: exact in any
+// order) and runs the row's epilogue.  Every value equals gemv_body's.
+// Preconditions (gemv_splitk_ok): four waves, every workgroup's four rows in
+// the one segment, one batch per wave.
+// ===========================================================================
+__device__ __forceinline__ int* splitk_lds() {
+  __shared__ int v[4 + 4 * 4];   // chunk maxima (float bits) [wave], row partials [wave][row]
+  return v;
+}
+__device__ __forceinline__ bool gemv_splitk_ok(const GemvArgs& a, int nblk, int nwv) {
+  return nwv == 4 && a.nseg == 1 && a.seg[0].batch0 == 0 && (a.seg[0].nbatch & 3) == 0 &&
+         a.seg[0].nbatch <= nblk * 4 && a.seg[0].kind == SEG_I8;
+}
+template <int NCH, int PRO, int KC, class IO>
+__device__ __forceinline__ bool gemv_splitk(const GemvArgs& a, int blk, IO& io) {
+  static_assert(NCH == 2 || NCH == 4, "two or four chunks per lane");
+  static_assert(PRO == P_LOAD || PRO == P_GATED, "prologue");
+  constexpr int EM = kEmResid;
+  constexpr int K = KC, nchunk = K / 16, RW = NCH;   // rows per wave
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int jw = wave % NCH, grp = wave / NCH;
+  const float* const ax = a.x;
+  const float* const anw = a.nw;
+  const float* const az = a.z;
+  const float eps = a.eps;
+  const int x_st = a.x_st, z_st = a.z_st, out_st = a.out_st;
+  const int total = __builtin_amdgcn_readfirstlane(a.seg[0].nbatch);
+  io.arrive();
+  io.mark(0);   // trace: stage entry
+  if (blk * 4 >= total) return true;   // no rows for this workgroup (workgroup-uniform)
+  typename IO::VecPoll vx;
+  io.stage_issue(ax, K, vx);
+  const Seg g = seg_uniform(a.seg[0]);
+  const int rb = __builtin_amdgcn_readfirstlane(blk * 4);
+  const int c = lane + 64 * jw;           // this lane's chunk
+  const int cc = min(c, nchunk - 1);
+  float nw16[16];
+  if constexpr (PRO == P_GATED) load16g(anw + ((16 * cc) & 127), nw16);   // the head's gains
+  // weights: rows rb + grp * RW + r, chunk c (clamped; a chunk past K meets x = 0)
+  uint32_t w[RW][4];
+  {
+    const __amdgpu_buffer_rsrc_t rw = rsrc_n(g.w, 0x7ffffff0);
+    const int last = g.rows - 1;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int row = __builtin_amdgcn_readfirstlane(min(rb + grp * RW + r, last));
+      const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rw, 16 * cc, row * K, kNt);
+      w[r][0] = t[0];
+      w[r][1] = t[1];
+      w[r][2] = t[2];
+      w[r][3] = t[3];
+    }
+  }
+  EpiAux aux;   // the output row of this wave, rb + wave
+  epi_prefetch<EM>(g, rb + wave, aux, io);
+  if (!io.wait()) return false;
+  float* xl = io.slot();
+  if (!io.stage_finish(ax, x_st, K, xl, vx)) return false;
+  const float* zl = nullptr;
+  if constexpr (PRO == P_GATED) {
+    float* buf = io.slot();
+    if (!io.stage_vec(az, z_st, K, buf)) return false;
+    zl = buf;
+  }
+  io.mark(1);   // trace: input vector in LDS
+  float xv[16];
+  load16l(xl + 16 * cc, xv);
+  if (c >= nchunk)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) xv[e] = 0.0f;
+  float amax = 0.0f;   // this lane's maximum |y| over its chunk
+  if constexpr (PRO == P_GATED) {   // heads of 128 = groups of 8 lanes; z holds silu(z); W8A8 order (x g) inv
+    float zs[16];
+    load16l(zl + 16 * cc, zs);
+    float ss = dot16_f32(xv, xv, 0.0f), mu = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      xv[e] = (xv[e] * nw16[e]) * zs[e];
+      mu = fmaxf(mu, fabsf(xv[e]));
+    }
+    ss = xor_sum<8>(ss);
+    mu = xor_max<8>(mu);   // this head's max |u|
+    const float inv = 1.0f / sqrtf(ss / 128.0f + eps);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) xv[e] = xv[e] * inv;
+    amax = mu * inv;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(xv[e]));
+  }
+  int* sk = splitk_lds();
+  {
+    const float cm = xor_max<64>(amax);   // the chunk's maximum
+    if (lane == 0) as_lds_w(sk)[wave] = __float_as_int(cm);
+  }
+  __syncthreads();
+  float am = 0.0f;   // _qa (golden/model.py:37-45): the vector's maximum
+#pragma unroll
+  for (int v = 0; v < 4; ++v) am = fmaxf(am, __int_as_float(as_lds(sk)[v]));
+  const float xs = quant_scale(am);
+  const float rs = 1.0f / xs;
+  uint32_t xq[4];
+  {
+    int q[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) q[e] = quant_one_r(xv[e], xs, rs);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) xq[d] = pack4(q[4 * d], q[4 * d + 1], q[4 * d + 2], q[4 * d + 3]);
+  }
+  io.mark(2);   // trace: prologue done
+  int pi[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) pi[r] = dot16_i8i8(w[r], xq, 0);
+  asm volatile("" ::"v"(pi[0]));
+  io.mark(5);   // trace: dot products done (the weights arrived)
+  {
+    // the four-row transposed butterfly (rows past RW are zero): lane l ends with
+    // row (l >> 4) & 3, and lanes 0, 16, 32, 48 write their rows' partials
+    int p4[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) p4[r] = r < RW ? pi[r] : 0;
+    const int part = reduce4(p4, lane);
+    const int prow = row_of_lane<4>(lane);
+    if ((lane & 15) == 0 && prow < RW) as_lds_w(sk)[4 + 4 * wave + prow] = part;
+  }
+  __syncthreads();
+  // row rb + wave: the partials of the NCH waves of its group, at its position in the group
+  int acci = 0;
+#pragma unroll
+  for (int jj = 0; jj < NCH; ++jj) acci += as_lds(sk)[4 + 4 * ((wave / NCH) * NCH + jj) + wave % NCH];
+  const int myrow = rb + wave;
+  const float y = ((float)acci * xs) * aux.sc;   // float(acc)*sx*sw
+  if (!io.resolve1(aux.res, g.res, g.res_st, min(myrow, g.rows - 1), aux.a0)) return false;
+  gemv_epilogue<1, EM>(g, out_st, lane, myrow, y, acci, aux, io);
+  io.mark(6);   // trace: row stored
   return true;
 }
 
