@@ -86,6 +86,27 @@ __device__ __forceinline__ float dev_softplus(float x) {
   return x > 20.0f ? x : dev_log1pf(dev_expf(x));
 }
 
+// Marks a loaded value as read without using it.  A load whose result is
+// never read keeps its registers pending; the next write to one of them -- at
+// the stage boundary, where the compiler cannot count the loads in flight --
+// then waits for every load and store of the wave.  Placed after a wait that
+// already covers the load (a later load's), it costs nothing.
+template <typename T>
+__device__ __forceinline__ void settle(const T& v) {
+  asm volatile("" ::"v"(v));
+}
+
+// Workgroup barrier for LDS hand-offs: the fences cover LDS only, so this
+// wave's global loads and stores stay in flight across it (__syncthreads()
+// orders global memory too).  Used where waves exchange only LDS data; vectors
+// produced by other workgroups arrive through tagged polls, which need no
+// ordering.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // gfx950's permlane swaps, written as inline assembly with both registers as
 // in/out operands: v_permlane32_swap a, b exchanges the upper 32 lanes of a with
 // the lower 32 lanes of b (afterwards a = [a.lo, b.lo], b = [a.hi, b.hi]);

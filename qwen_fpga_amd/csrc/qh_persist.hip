@@ -24,9 +24,13 @@ namespace qh {
 // load whose wait also waits for every load and store issued before it.  The
 // copy of stage i + 1 is loaded (one word per thread) at the start of stage i,
 // ahead of that stage's own loads, and written to the other of two LDS slots
-// at the start of stage i + 1, followed by one workgroup barrier.  A slot is
-// rewritten two stages after it was filled; every wave has passed the barrier
-// of the stage in between, so no wave still reads it.
+// at stage i's first tag check (TagIO::desc_put), or at the start of stage
+// i + 1 by a thread that checked no tag in stage i; then one LDS-only
+// workgroup barrier.  A slot is rewritten one stage after it was read: every
+// wave has passed the barrier at the start of the stage in between, so no
+// wave still reads it.  No global memory is exchanged through the barrier:
+// the stage stores stay in flight into the next stage (their consumers poll
+// tags), and the head stage orders the token's stores before its partials.
 constexpr int kStageWords = (int)(sizeof(Stage) / 4);
 static_assert(sizeof(Stage) % 4 == 0 && kStageWords <= kPersistThreads, "one descriptor word per thread");
 
@@ -58,14 +62,14 @@ __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistA
   if (P.dn_lds) dn_tiles_copy(P.prog, P.nstage, blk, nblk, true);   // this workgroup's DeltaNet state tiles
 
   const uint32_t* progw = reinterpret_cast<const uint32_t*>(P.prog);
-  uint32_t nxt = t < kStageWords ? progw[t] : 0u;   // descriptor word of stage 0
+  io.desc_next(progw, s_stage[0], kStageWords);   // descriptor of stage 0
   int slot = 0;
   for (int k = 0;; ++k) {
     io.tag0 = P.tag_base + (uint32_t)k * (uint32_t)kTagsPerToken;
     for (int i = 0; i < P.nstage; ++i) {
-      if (t < kStageWords) s_stage[slot][t] = nxt;
+      io.desc_put();   // (a thread that checked no tag in the previous stage)
       if (io.failed) s_fail[slot] = 1;
-      __syncthreads();
+      lds_barrier();
       if (s_fail[slot] != 0) {   // workgroup-uniform: read after the barrier
         aborted = 1;
         break;
@@ -73,7 +77,7 @@ __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistA
       const Stage& st = *reinterpret_cast<const Stage*>(s_stage[slot]);
       slot ^= 1;
       const int ni = i + 1 < P.nstage ? i + 1 : 0;   // the next stage (stage 0 after the head)
-      nxt = t < kStageWords ? progw[(size_t)ni * kStageWords + t] : 0u;
+      io.desc_next(progw + (size_t)ni * kStageWords, s_stage[slot], kStageWords);
       asm volatile("" ::: "memory");   // issued before any load of this stage
       uint64_t* tr = (P.trace != nullptr && k < P.trace_tokens) ? P.trace + (((size_t)k * P.nstage + i) * nblk + blk) * kTraceSlots : nullptr;
       io.tr = tr;

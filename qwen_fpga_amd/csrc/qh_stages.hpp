@@ -275,6 +275,28 @@ struct TagIO {
   __device__ __forceinline__ uint32_t tag(int st) const { return tag0 + (uint32_t)st; }
   __device__ __forceinline__ void arrive() {}
   __device__ __forceinline__ bool wait() { return true; }
+  // The persistent kernel's next stage descriptor: each thread's word of it is
+  // loaded at the start of a stage (desc_next) and written to its LDS slot at
+  // the stage's first tag check (desc_put).  The poll being checked was issued
+  // after the descriptor load and a wave's loads return in order, so the write
+  // waits for nothing more.  Written at the stage boundary instead, it would
+  // wait for every load and store of the stage (the compiler cannot count
+  // them across the stage bodies), the stores' acknowledgements included.
+  uint32_t dword = 0;
+  __attribute__((address_space(3))) uint32_t* ddst = nullptr;   // nullptr: no word for this thread
+  bool dpend = false;
+  __device__ __forceinline__ void desc_next(const uint32_t* src, uint32_t* slot, int nwords) {
+    const int t = threadIdx.x;
+    ddst = t < nwords ? as_lds_w(slot + t) : nullptr;
+    if (t < nwords) dword = src[t];
+    dpend = true;
+  }
+  __device__ __forceinline__ void desc_put() {
+    if (dpend) {
+      if (ddst != nullptr) *ddst = dword;
+      dpend = false;
+    }
+  }
   // After a failed poll: false (and the wave marked failed) once the limit is
   // reached or another wave gave up.  A failed wave polls no more.
   __device__ __forceinline__ bool again(unsigned& polls) {
@@ -327,7 +349,9 @@ struct TagIO {
     const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
     u32x4 u[N][8];
     issue16<N>(rs, idx, u);
-    if (!tags16<N>(u, tg)) {
+    const bool hit = tags16<N>(u, tg);
+    desc_put();
+    if (!hit) {
       unsigned polls = 0;
       do {   // after a miss, wait on one pair per lane before loading everything again
         if (!again(polls) || !sample(rs, idx[N - 1] + 15, tg, polls)) break;   // gave up: stale values
@@ -360,7 +384,9 @@ struct TagIO {
       return wave_all(ok);
     };
     issue();
-    if (!tags()) {
+    const bool hit = tags();
+    desc_put();
+    if (!hit) {
       unsigned polls = 0;
       do {
         if (!again(polls)) break;   // gave up: stale values
@@ -393,7 +419,9 @@ struct TagIO {
     return r;
   }
   __device__ __forceinline__ bool resolve1(const Raw& r, const float* base, int st, int idx, float& v) {
-    if (wave_all(r.t == tag(st))) {
+    const bool hit = wave_all(r.t == tag(st));
+    desc_put();
+    if (hit) {
       v = __uint_as_float(r.v);
       return true;
     }
@@ -436,6 +464,7 @@ struct TagIO {
       return tags16<N>(P.u, tg) && wave_all(ok);
     };
     const bool hit = tags();
+    desc_put();
     mark(3);   // trace: first poll returned
     if (!hit) {
       const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
@@ -492,6 +521,7 @@ struct TagIO {
       return wave_all(ok);
     };
     const bool hit = tags();
+    desc_put();
     mark(3);   // trace: first poll returned
     if (!hit) {
       const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
@@ -578,6 +608,7 @@ struct TagIO {
     const uint32_t tg = tag(st);
     const int t = threadIdx.x, lane = t & 63;
     const bool hit = vec_tags(vp, K, tg);
+    desc_put();
     mark(3);   // trace: first poll returned
     if (!hit) {
       const __amdgpu_buffer_rsrc_t rs = coh_rsrc(base);
@@ -771,6 +802,12 @@ struct EpiAux {
   float sc = 1.0f;                                     // the row's weight scale (int8 segments)
   Raw res;                                             // E_RESID: residual, resolved before use
 };
+// every input epi_prefetch loaded, read or not by the segment's epilogue
+__device__ __forceinline__ void settle_aux(const EpiAux& x) {
+  settle(x.a0), settle(x.a1), settle(x.a2), settle(x.a3);
+  settle(x.w0), settle(x.w1), settle(x.w2), settle(x.w3);
+  settle(x.sc), settle(x.res.v), settle(x.res.t);
+}
 // Every input an epilogue may need, loaded without a branch: inputs the
 // segment's epilogue does not use come from zero-size descriptors (no memory
 // access), so the load block stays straight-line and the compiler can count
@@ -992,7 +1029,8 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
   // ---------------- 1. the first poll of x, then weights and epilogue inputs of the first batch
   // One straight-line block issues every load of the first batch: the first
   // poll of x, the norm gains, the gate row, the weights and the epilogue
-  // inputs.  Waves without rows load the workgroup's last batch and drop it.
+  // inputs.  Waves without rows load the workgroup's last batch and drop it
+  // (settled before they leave).
   const bool stage_x = PRO != P_LOADQ && !(PRO == P_NORM && aemb != nullptr);
   typename IO::VecPoll vx;
   if constexpr (PRO != P_LOADQ) io.stage_issue(ax, stage_x ? K : 0, vx);
@@ -1230,7 +1268,21 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
       if (lane == 0) io.st1(agout, out_st, 16 * hh + (grow < 16 ? 1 : 0), val);
     }
   }
-  if (b >= total) return true;   // no rows for this wave (it took part in the barriers above)
+  if (b >= total) {   // no rows for this wave (it took part in the barriers above)
+#pragma unroll
+    for (int j = 0; j < NCH; ++j)
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) settle(w[j][r][d]);
+    settle_aux(aux);
+    if constexpr (PRO == P_NORM && NCH == 1) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) settle(gwv[e]);
+      settle(g_alog), settle(g_dtb);
+    }
+    return true;
+  }
   const int b0 = b;
   // ---------------- 3. row batches (the next batch's loads overlap this batch's reduction)
   for (; b < total; b += stride) {
@@ -1282,6 +1334,11 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
         asm volatile("" ::"v"(pf[0]));
       }
       io.mark(5);
+      if constexpr (PRO == P_NORM && NCH == 1) {   // the gate loads (issued before the weights) of other waves
+#pragma unroll
+        for (int e = 0; e < 16; ++e) settle(gwv[e]);
+        settle(g_alog), settle(g_dtb);
+      }
     }
     // issue the next batch's loads before reducing this one
     const int bn = b + stride;
@@ -1306,6 +1363,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
         !io.resolve1(aux.res, g.res, g.res_st, min(myrow, g.rows - 1), aux.a0))
       return false;
     gemv_epilogue<R, EM>(g, out_st, lane, myrow, y, acci, aux, io);
+    settle_aux(aux);   // inputs this segment's epilogue did not read
     if (b == b0) io.mark(6);   // trace: first batch stored
     si = sin;
     g = gn;
@@ -1459,6 +1517,7 @@ __device__ __forceinline__ bool gemv_splitk(const GemvArgs& a, int blk, IO& io) 
   const float y = ((float)acci * xs) * aux.sc;   // float(acc)*sx*sw
   if (!io.resolve1(aux.res, g.res, g.res_st, min(myrow, g.rows - 1), aux.a0)) return false;
   gemv_epilogue<1, EM>(g, out_st, lane, myrow, y, acci, aux, io);
+  settle_aux(aux);   // inputs this segment's epilogue did not read
   io.mark(6);   // trace: row stored
   return true;
 }
