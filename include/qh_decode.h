@@ -149,8 +149,8 @@ int qh_mlp_layer(float* out, const float* x, const qh_tensor* gate_w, const qh_t
  * allocation: no counterpart in the reference; for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
  * arguments, kernels and results; the intermediate vectors live in one file-scope device array
- * of the library (4.3 MB on every GPU the library runs on, held until the process ends), so
- * T + 1 <= 8192 -- the reference's own sc[8192] bound (attention.hpp:66) -- else QH_ERANGE.
+ * of the library (1.1 MB on every GPU the library runs on, held until the process ends), so
+ * T + 1 <= 65536 (above the reference's own sc[8192] bound, attention.hpp:66), else QH_ERANGE.
  * Every call on one GPU uses that GPU's array: calls that overlap on one GPU (other streams,
  * other host threads) race and must be serialised by the caller. */
 int qh_attention_layer_noalloc(float* out, const float* x, const qh_tensor* q_w, const qh_tensor* k_w,

@@ -38,6 +38,11 @@
 #define N_FULL 6
 /* device-order constants: attention positions per split, DeltaNet k-groups */
 #define DEV_ATTN_SPLIT 16
+/* longer contexts (Tn > DEV_ATTN_SHORT_MAX): splits of dev_attn_split_len(Tn) positions */
+#define DEV_ATTN_SHORT_MAX 2048
+#define DEV_ATTN_MAX_SPLITS 128
+#define DEV_ATTN_MAX_SPLIT_LEN 512
+#define DEV_ATTN_LONG_D 4
 #define DEV_DN_KGROUPS 8
 
 static int is_linear(int layer) { return (layer % 4) != 3; }   /* types.hpp:47 */
@@ -689,6 +694,93 @@ static void attn_core_dev(float* og, const float* q, const float* gate, const fl
   free(accs);
 }
 
+/* device order for Tn > DEV_ATTN_SHORT_MAX (qh_stages.hpp attn_unit_long / combine_long).
+ * P = 4*ceil(Tn/512) positions per split (at most 512).  Per split and head the four
+ * waves w take the iterations it = w, w+4, ... of four positions t0+4it+u, kw per wave
+ * (rounded up to a multiple of 4); wave w: m_w the maximum score of its positions,
+ * then in its order (k ascending, then u) p = exp(s - m_w) (0 past the split's end,
+ * where v is the split's last row), l_w = l_w + p, acc_w = fma(p, v, acc_w).  Merge:
+ * M = max m_w, e_w = exp(m_w - M) (0 for m_w = -inf), l = (l0 e0 + l1 e1) + (l2 e2 +
+ * l3 e3), acc likewise.  Combine: M = max m_s, e_s = exp(m_s - M); quarter w of the
+ * splits [w c, (w+1) c), c = ceil(ns/4), folded in order (L = L + l e, ctx = ctx +
+ * acc e); L = (L0 + L1) + (L2 + L3), ctx the same; ctx * (1/L) * sigmoid(gate). */
+static int dev_attn_split_len(int Tn) {
+  if (Tn <= DEV_ATTN_SHORT_MAX) return DEV_ATTN_SPLIT;
+  const int P = 4 * ((Tn + 4 * DEV_ATTN_MAX_SPLITS - 1) / (4 * DEV_ATTN_MAX_SPLITS));
+  return P < DEV_ATTN_MAX_SPLIT_LEN ? P : DEV_ATTN_MAX_SPLIT_LEN;
+}
+static void attn_core_dev_long(float* og, const float* q, const float* gate, const float* kcache,
+                               const float* vcache, int Tn) {
+  const int rep = NH / NKV, P = dev_attn_split_len(Tn), D = DEV_ATTN_LONG_D;
+  const int ns = (Tn + P - 1) / P;
+  float* ms = (float*)malloc(sizeof(float) * (size_t)ns);
+  float* ls = (float*)malloc(sizeof(float) * (size_t)ns);
+  float* accs = (float*)malloc(sizeof(float) * (size_t)ns * HD);
+  float* sc = (float*)malloc(sizeof(float) * (size_t)P);
+  for (int h = 0; h < NH; ++h) {
+    const int kv = h / rep;
+    for (int s = 0; s < ns; ++s) {
+      const int t0 = s * P, t1 = t0 + P < Tn ? t0 + P : Tn;
+      const int nit = (t1 - t0 + 3) / 4, kw = ((nit + 3) / 4 + D - 1) / D * D;
+      for (int t = t0; t < t1; ++t)
+        sc[t - t0] = c16_dot_f32(q + h * HD, kcache + (long)t * KV_PROJ + kv * HD, HD) * 0.0625f;
+      float mw[4], lw[4], aw[4][HD];
+      for (int w = 0; w < 4; ++w) {
+        float m = -INFINITY;
+        for (int k = 0; k < kw; ++k)
+          for (int u = 0; u < 4; ++u) {
+            const int t = t0 + 4 * (w + 4 * k) + u;
+            if (t < t1 && sc[t - t0] > m) m = sc[t - t0];
+          }
+        float l = 0.0f;
+        for (int d = 0; d < HD; ++d) aw[w][d] = 0.0f;
+        for (int k = 0; k < kw; ++k)
+          for (int u = 0; u < 4; ++u) {
+            const int t = t0 + 4 * (w + 4 * k) + u;
+            const float p = t < t1 ? or_dev_expf(sc[t - t0] - m) : 0.0f;
+            const float* vt = vcache + (long)(t < t1 ? t : t1 - 1) * KV_PROJ + kv * HD;
+            for (int d = 0; d < HD; ++d) aw[w][d] = fmaf(p, vt[d], aw[w][d]);
+            l = l + p;
+          }
+        mw[w] = m;
+        lw[w] = l;
+      }
+      float M = -INFINITY, e[4];
+      for (int w = 0; w < 4; ++w)
+        if (mw[w] > M) M = mw[w];
+      for (int w = 0; w < 4; ++w) e[w] = mw[w] == -INFINITY ? 0.0f : or_dev_expf(mw[w] - M);
+      ms[s] = M;
+      ls[s] = (lw[0] * e[0] + lw[1] * e[1]) + (lw[2] * e[2] + lw[3] * e[3]);
+      for (int d = 0; d < HD; ++d)
+        accs[(size_t)s * HD + d] = (aw[0][d] * e[0] + aw[1][d] * e[1]) + (aw[2][d] * e[2] + aw[3][d] * e[3]);
+    }
+    float M = -INFINITY;
+    for (int s = 0; s < ns; ++s)
+      if (ms[s] > M) M = ms[s];
+    const int c = (ns + 3) / 4;
+    float Lq[4], cq[4][HD];
+    for (int w = 0; w < 4; ++w) {
+      const int s0 = w * c < ns ? w * c : ns, s1 = s0 + c < ns ? s0 + c : ns;
+      Lq[w] = 0.0f;
+      for (int d = 0; d < HD; ++d) cq[w][d] = 0.0f;
+      for (int s = s0; s < s1; ++s) {
+        const float es = or_dev_expf(ms[s] - M);
+        Lq[w] = Lq[w] + ls[s] * es;
+        for (int d = 0; d < HD; ++d) cq[w][d] = cq[w][d] + accs[(size_t)s * HD + d] * es;
+      }
+    }
+    const float invL = 1.0f / ((Lq[0] + Lq[1]) + (Lq[2] + Lq[3]));
+    for (int d = 0; d < HD; ++d) {
+      const float ctx = (cq[0][d] + cq[1][d]) + (cq[2][d] + cq[3][d]);
+      og[h * HD + d] = (ctx * invL) * or_sigmoid(gate[h * HD + d], OR_ORDER_DEV);
+    }
+  }
+  free(ms);
+  free(ls);
+  free(accs);
+  free(sc);
+}
+
 void or_attention_layer(float* out, const float* x, const or_tensor* q_w, const or_tensor* k_w,
                         const or_tensor* v_w, const or_tensor* o_w, const float* q_norm,
                         const float* k_norm, int pos, float* kcache, float* vcache, int T, int mode,
@@ -717,7 +809,9 @@ void or_attention_layer(float* out, const float* x, const or_tensor* q_w, const 
     for (int d = 0; d < HD; ++d) kslot[kv * HD + d] = ktmp[d];
     for (int d = 0; d < HD; ++d) vslot[kv * HD + d] = vflat[kv * HD + d];
   }
-  if (order == OR_ORDER_DEV)
+  if (order == OR_ORDER_DEV && T + 1 > DEV_ATTN_SHORT_MAX)
+    attn_core_dev_long(og, q, gate, kcache, vcache, T + 1);
+  else if (order == OR_ORDER_DEV)
     attn_core_dev(og, q, gate, kcache, vcache, T + 1);
   else
     attn_core_ref(og, q, gate, kcache, vcache, T + 1);

@@ -287,7 +287,7 @@ def attention_layer(out, x, q_w: Tensor, k_w: Tensor, v_w: Tensor, o_w: Tensor, 
 
 def attention_layer_noalloc(out, x, q_w: Tensor, k_w: Tensor, v_w: Tensor, o_w: Tensor, q_norm, k_norm, pos: int,
                             kcache, vcache, T: int, w8a8: bool = False, stream=None):
-    """attention_layer without any device allocation (the library's static scratch; T + 1 <= 8192)."""
+    """attention_layer without any device allocation (the library's static scratch; T + 1 <= 65536)."""
     n_kv = (max(T, 0) + 1) * 512
     _call("qh_attention_layer_noalloc", _dev(out, "f32", HIDDEN, "out"), _dev(x, "f32", HIDDEN, "x"), q_w, k_w,
           v_w, o_w, _dev(q_norm, "f32", 256, "q_norm"), _dev(k_norm, "f32", 256, "k_norm"), pos,

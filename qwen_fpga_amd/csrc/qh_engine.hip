@@ -697,7 +697,7 @@ int create(const void* blob, size_t blob_len, const char* idx_text, int max_ctx,
     const unsigned long long v = std::strtoull(ts, nullptr, 10);
     if (v >= 1 && v <= 0xFFFFFFFFull) e->tag_start = (uint32_t)v;
   }
-  e->nsplit_max = (max_ctx + kAttnSplit - 1) / kAttnSplit;
+  e->nsplit_max = attn_nsplit_max(max_ctx);
   e->head_grid = kVocab / (kRowsPerBatch * 4 * 4);   // 4 waves x 4 batches per block
   int st = QH_OK;
 #define QH_C(expr)             \

@@ -7,7 +7,27 @@
 namespace qh {
 
 constexpr int kRowsPerBatch = 8;     // rows one wave reduces together (LM head, large GEMVs)
-constexpr int kAttnSplit = 16;       // positions per attention split
+constexpr int kAttnSplit = 16;       // positions per attention split, contexts up to kAttnShortMax
+// Longer contexts: splits of attn_split_len(Tn) positions, a multiple of 4 and
+// at most kAttnMaxSplitLen, so that there are at most kAttnMaxSplits splits per
+// kv head up to 65536 positions (the units fill the GPU once; the split
+// partials are 2 / P of the cache bytes).
+constexpr int kAttnShortMax = 2048;
+constexpr int kAttnMaxSplits = 128;
+constexpr int kAttnMaxSplitLen = 512;
+// positions per split for a context of Tn positions (the slot of this token included)
+__host__ __device__ constexpr int attn_split_len(int Tn) {
+  return Tn <= kAttnShortMax ? kAttnSplit
+                             : (4 * ((Tn + 4 * kAttnMaxSplits - 1) / (4 * kAttnMaxSplits)) < kAttnMaxSplitLen
+                                    ? 4 * ((Tn + 4 * kAttnMaxSplits - 1) / (4 * kAttnMaxSplits))
+                                    : kAttnMaxSplitLen);
+}
+__host__ __device__ constexpr int attn_nsplit(int Tn) { return (Tn + attn_split_len(Tn) - 1) / attn_split_len(Tn); }
+// the most splits any context up to max_ctx positions takes (buffer sizes)
+__host__ __device__ constexpr int attn_nsplit_max(int max_ctx) {
+  return max_ctx <= kAttnShortMax ? (max_ctx + kAttnSplit - 1) / kAttnSplit
+                                  : (attn_nsplit(max_ctx) > kAttnMaxSplits ? attn_nsplit(max_ctx) : kAttnMaxSplits);
+}
 constexpr int kDnVQuarters = 4;      // DeltaNet workgroups per head (32 v columns each)
 constexpr int kDnSlots = 5;          // persistent kernel: DeltaNet state tiles per workgroup (LDS)
 

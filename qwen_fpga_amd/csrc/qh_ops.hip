@@ -83,14 +83,15 @@ constexpr size_t attention_scratch_bytes(int ns) {
 }
 
 // ---- the scratch of qh_attention_layer_noalloc: one file-scope device array ----
-// Contexts up to the reference's own bound, sc[8192] (attention.hpp:66): T + 1 <= 8192,
-// 512 splits of 16 positions: 4.3 MB held on every GPU the library runs on until the
-// process ends.  In host code `scratch` names a host-side stand-in, not the device
+// Contexts up to 65536 positions (T + 1 <= 65536; above the reference's own bound,
+// sc[8192], attention.hpp:66): at most kAttnMaxSplits splits, 1.1 MB held on every GPU
+// the library runs on until the process ends.  In host code `scratch` names a host-side stand-in, not the device
 // array: its device address is taken once per device (hipGetSymbolAddress, with that
 // device current) and only that address reaches kernels.
-constexpr int kNoallocMaxCtx = 8192;
-constexpr size_t kNoallocBytes = attention_scratch_bytes(kNoallocMaxCtx / kAttnSplit);
-static_assert(kNoallocMaxCtx % kAttnSplit == 0 && kNoallocBytes < (size_t)5 << 20, "a modest, fixed maximum");
+constexpr int kNoallocMaxCtx = 65536;
+constexpr size_t kNoallocBytes = attention_scratch_bytes(attn_nsplit_max(kNoallocMaxCtx));
+static_assert(attn_nsplit_max(kNoallocMaxCtx) == kAttnMaxSplits && kNoallocBytes < (size_t)2 << 20,
+              "a modest, fixed maximum");
 __device__ __align__(256) char scratch[kNoallocBytes];
 constexpr int kMaxDevices = 64;
 char* g_scratch_dev[kMaxDevices] = {};
@@ -206,7 +207,7 @@ int attention_layer(float* out, const float* x, const qh_tensor* q_w, const qh_t
   if (!aligned16(x) || !aligned16(q_norm) || !aligned16(k_norm) || !aligned16(kcache) || !aligned16(vcache))
     return QH_EINVAL;
   const int Tn = T + 1;
-  const int ns = (Tn + kAttnSplit - 1) / kAttnSplit;
+  const int ns = attn_nsplit(Tn);
   Scratch sc(s, given, given_size);
   QH_TRY(sc.alloc(attention_scratch_bytes(ns)));
   float* qkv = sc.take<float>(kQProj + 2 * kKVProj);   // q||gate | k | v
@@ -488,8 +489,7 @@ int qh_attention_layer_noalloc(float* out, const float* x, const qh_tensor* q_w,
   if (T < 0 || T + 1 > kNoallocMaxCtx) return QH_ERANGE;
   char* base = nullptr;
   QH_TRY(noalloc_scratch(&base));
-  const int ns = (T + 1 + kAttnSplit - 1) / kAttnSplit;
-  if (attention_scratch_bytes(ns) > kNoallocBytes) return QH_ERANGE;
+  if (attention_scratch_bytes(attn_nsplit(T + 1)) > kNoallocBytes) return QH_ERANGE;
   return attention_layer(out, x, q_w, k_w, v_w, o_w, q_norm, k_norm, pos, kcache, vcache, T,
                          mode == QH_MODE_W8A8 ? M_W8A8 : M_W8A16, S(stream), base, kNoallocBytes);
 }

@@ -2089,20 +2089,266 @@ __device__ __forceinline__ bool attn_unit(const AttnArgs& a, int s, int j, int T
   return true;
 }
 
+// ===========================================================================
+// Long contexts (Tn = T + 1 > kAttnShortMax): splits of P = attn_split_len(Tn)
+// positions.  Unit (split s, kv head j): wave w of the workgroup takes the
+// iterations it = w, w + 4, ... of four positions t0 + 4 it + pg and computes
+// all four query heads of kv head j on them, so a K or V row is read once per
+// workgroup (and 2 / P of the cache bytes go to split partials).
+//   pass 1  the K rows: the scores of (head, position) into LDS, and the
+//           wave's maximum m_w per head;
+//   pass 2  the V rows in the wave's position order (k ascending, then pg):
+//           p = exp(s - m_w), l_w = l_w + p, acc_w = fma(p, v, acc_w);
+//   merge   M = max m_w, e_w = exp(m_w - M) (0 for a wave without positions),
+//           l = (l0 e0 + l1 e1) + (l2 e2 + l3 e3), acc the same; wave w stores
+//           the partial of query head 4 j + w.
+// Every wave runs kw iterations (the split's iterations per wave, rounded up to
+// a multiple of kAttnLongD, the same for all four waves).  A position at or past
+// the split's end has the score -inf and p = 0; its K / V loads re-read the
+// split's last row, and fma(0, v, acc) and l + 0 leave acc and l unchanged.
+// The loads stay straight-line: each unrolled step uses the rows loaded
+// kAttnLongD steps earlier and issues the loads of kAttnLongD steps later.
+// ===========================================================================
+constexpr int kAttnLongD = 4;   // iterations of K rows in flight per wave (V: 4 rows per iteration)
+
+template <bool OWNER, class IO>
+__device__ __forceinline__ bool attn_unit_long(const AttnArgs& a, int s, int j, int T, int rrow, IO& io) {
+  constexpr int D = kAttnLongD;
+  constexpr int kBig = 0x7ffffff0;
+  const int Tn = T + 1;
+  const int P = attn_split_len(Tn);
+  const int lane = threadIdx.x & 63, g16 = lane & 15, pg = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = 4 * j + w;   // the query head this wave normalises, and stores after the merge
+  const int t0 = s * P, t1 = min(t0 + P, Tn), tlast = t1 - 1;
+  const int nit = (t1 - t0 + 3) >> 2;                     // iterations of the split
+  const int kw = ((nit + 3) / 4 + D - 1) / D * D;         // per wave, padded
+  // inputs: the query of head h (two 128-element regions); the owner also takes
+  // the new K and V rows of kv head j (two regions each), as the short unit
+  constexpr int NR = OWNER ? 6 : 2;
+  int reg[NR];
+  reg[0] = h * 512;
+  reg[1] = h * 512 + 128;
+  if constexpr (OWNER) {
+    reg[2] = 4096 + j * 256;
+    reg[3] = 4096 + j * 256 + 128;
+    reg[4] = 4608 + j * 256;
+    reg[5] = 4608 + j * 256 + 128;
+  }
+  const int iv[1] = {h * 512 + lane};
+  typename IO::template PollR<NR, 1> Pq;
+  io.template pollr_issue<NR, 1>(a.qkv, reg, iv, Pq);
+  const __amdgpu_buffer_rsrc_t rk = rsrc_n(a.kc, kBig);
+  const __amdgpu_buffer_rsrc_t rv = rsrc_n(a.vc, kBig);
+  auto row = [&](int k, int u) { return min(t0 + 4 * (w + 4 * k) + u, tlast); };   // position, clamped
+  float kb[D][16];   // K: 16 dims (16 g16 ..) of position t0 + 4 (w + 4 k) + pg
+#pragma unroll
+  for (int d = 0; d < D; ++d) load16_rs(rk, (row(d, pg) * 512 + j * 256 + 16 * g16) * 4, kb[d]);
+  float qn16[16], kn16[16], cs16[16], sn16[16];
+  load16_rs(rsrc_n(a.qn, kBig), 64 * g16, qn16);
+  load16_rs(rsrc_n(a.kn, kBig), 64 * g16, kn16);
+  {
+    const __amdgpu_buffer_rsrc_t rr = rsrc_n(a.rope, kBig);
+    load16_rs(rr, (rrow * 64 + 16 * (g16 & 1)) * 4, cs16);
+    load16_rs(rr, (rrow * 64 + 32 + 16 * (g16 & 1)) * 4, sn16);
+  }
+  if (!io.wait()) return false;
+  float* wa = wave_area();
+  float unused[1];
+  if (!io.template pollr_finish<NR, 1>(a.qkv, a.qkv_st, reg, iv, Pq, wa, unused)) return false;
+  float qh[16], knew[16], vnew[4];
+  load16l(wa + 16 * g16, qh);
+  if constexpr (OWNER) {
+    load16l(wa + 256 + 16 * g16, knew);
+    const f32x4 t = *as_lds(reinterpret_cast<const f32x4*>(wa + 512 + 4 * lane));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) vnew[e] = t[e];
+    qk_norm_rope(knew, kn16, a.eps, g16, cs16, sn16);
+    if (w == 0) {   // wave 0 writes the new cache rows
+      if (pg == 0) stc16(a.kc, T * 512 + j * 256 + 16 * g16, knew);
+      stc4(a.vc, T * 512 + j * 256 + 4 * lane, vnew);
+    }
+  }
+  io.mark(1);   // trace: q (and the new k, v) received
+  qk_norm_rope(qh, qn16, a.eps, g16, cs16, sn16);
+  // the four normalised queries meet in LDS
+  float* ql = io.slot();   // [4 heads][256]
+  float* sc = io.slot();   // [4 waves][4 heads][4 kw]: scores, then p
+  if (pg == 0) {
+#pragma unroll
+    for (int e = 0; e < 16; e += 4)
+      *as_lds_w(reinterpret_cast<f32x4*>(ql + w * 256 + 16 * g16 + e)) = f32x4{qh[e], qh[e + 1], qh[e + 2], qh[e + 3]};
+  }
+  lds_barrier();
+  float q[4][16];
+#pragma unroll
+  for (int hh = 0; hh < 4; ++hh) load16l(ql + hh * 256 + 16 * g16, q[hh]);
+  // ---- pass 1: scores and the wave's maxima
+  float m[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+  float* scw = sc + w * 16 * kw;
+  for (int k0 = 0; k0 < kw; k0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int k = k0 + d;
+      const int t = t0 + 4 * (w + 4 * k) + pg;
+      float kv[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) kv[e] = kb[d][e];
+      if constexpr (OWNER) {
+        const bool sel = t == T;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) kv[e] = sel ? knew[e] : kv[e];
+      }
+      load16_rs(rk, (row(k + D, pg) * 512 + j * 256 + 16 * g16) * 4, kb[d]);   // k + D (clamped)
+#pragma unroll
+      for (int hh = 0; hh < 4; ++hh) {
+        float dd = dot16_f32(q[hh], kv, 0.0f);
+        dd = xor_sum<16>(dd);
+        const float sv = t < t1 ? dd * 0.0625f : -__builtin_inff();
+        m[hh] = fmaxf(m[hh], sv);
+        if (g16 == hh) as_lds_w(scw)[(hh * kw + k) * 4 + pg] = sv;
+      }
+    }
+  }
+#pragma unroll
+  for (int hh = 0; hh < 4; ++hh) {
+    m[hh] = fmaxf(m[hh], xor_perm<16>(m[hh]));
+    m[hh] = fmaxf(m[hh], xor_perm<32>(m[hh]));
+  }
+  // ---- V rows of the first D iterations, then p of this wave's positions (lane-parallel)
+  float vb[D][4][4];
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rv, (row(d, u) * 512 + j * 256 + 4 * lane) * 4, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) vb[d][u][e] = __uint_as_float(t[e]);
+    }
+#pragma unroll
+  for (int hh = 0; hh < 4; ++hh)
+    for (int i = lane; i < 4 * kw; i += 64) {
+      auto* c = as_lds_w(scw) + hh * 4 * kw + i;
+      const float sv = *c;
+      *c = sv == -__builtin_inff() ? 0.0f : dev_expf(sv - m[hh]);   // past the split's end: 0 (m may be -inf)
+    }
+  // ---- pass 2: p . V in the wave's position order
+  float acc[4][4], l[4];
+#pragma unroll
+  for (int hh = 0; hh < 4; ++hh) {
+    l[hh] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[hh][e] = 0.0f;
+  }
+  for (int k0 = 0; k0 < kw; k0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int k = k0 + d;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int t = t0 + 4 * (w + 4 * k) + u;
+        float vv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vv[e] = vb[d][u][e];
+        if constexpr (OWNER) {
+          const bool sel = t == T;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) vv[e] = sel ? vnew[e] : vv[e];
+        }
+        const u32x4 nv =
+            __builtin_amdgcn_raw_buffer_load_b128(rv, (row(k + D, u) * 512 + j * 256 + 4 * lane) * 4, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vb[d][u][e] = __uint_as_float(nv[e]);
+#pragma unroll
+        for (int hh = 0; hh < 4; ++hh) {
+          const float pu = as_lds(scw)[(hh * kw + k) * 4 + u];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[hh][e] = __builtin_fmaf(pu, vv[e], acc[hh][e]);
+          l[hh] = l[hh] + pu;
+        }
+      }
+    }
+  }
+  // the last refills re-read the split's last row: read (they returned with the rows used above)
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) settle(kb[d][e]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) settle(vb[d][u][e]);
+  }
+  // ---- merge of the four waves: heads 0, 1 in one slot, heads 2, 3 in the next
+  float* mg[2];
+  mg[0] = io.slot();
+  mg[1] = io.slot();
+#pragma unroll
+  for (int hh = 0; hh < 4; ++hh) {
+    float* r = mg[hh >> 1];
+    const int hl = hh & 1;
+    *as_lds_w(reinterpret_cast<f32x4*>(r + 16 + (w * 2 + hl) * 256 + 4 * lane)) =
+        f32x4{acc[hh][0], acc[hh][1], acc[hh][2], acc[hh][3]};
+    if (lane == 0) {
+      as_lds_w(r)[(w * 2 + hl) * 2] = m[hh];
+      as_lds_w(r)[(w * 2 + hl) * 2 + 1] = l[hh];
+    }
+  }
+  lds_barrier();
+  {
+    const float* r = mg[w >> 1];
+    const int hl = w & 1;
+    float mw[4], lw[4], ew[4];
+    float M = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      mw[i] = as_lds(r)[(i * 2 + hl) * 2];
+      lw[i] = as_lds(r)[(i * 2 + hl) * 2 + 1];
+      M = fmaxf(M, mw[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ew[i] = mw[i] == -__builtin_inff() ? 0.0f : dev_expf(mw[i] - M);
+    const float L = (lw[0] * ew[0] + lw[1] * ew[1]) + (lw[2] * ew[2] + lw[3] * ew[3]);
+    float A[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 t = *as_lds(reinterpret_cast<const f32x4*>(r + 16 + (i * 2 + hl) * 256 + 4 * lane));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) A[i][e] = t[e];
+    }
+    float out[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[e] = (A[0][e] * ew[0] + A[1][e] * ew[1]) + (A[2][e] * ew[2] + A[3][e] * ew[3]);
+    if (lane == 0) {
+      io.st1(a.pm, a.part_st, h * a.nsplit_max + s, M);
+      io.st1(a.pl, a.part_st, h * a.nsplit_max + s, L);
+    }
+    io.mark(2);   // trace: the split's partials merged
+    io.st4(a.pacc, a.part_st, (h * a.nsplit_max + s) * 256 + 4 * lane, out);
+  }
+  return true;
+}
+
 // Units u = blk, blk + nblk, ... of the 2 * ceil((T+1)/16) splits; T is the slot
 // of this token (past tokens = T).
 template <class IO>
 __device__ __forceinline__ bool attn_body(const AttnArgs& a, int T, int blk, int nblk, IO& io) {
   const bool ok = T >= 0 && T < a.max_ctx;
-  const int units = ok ? 2 * ((T + 1 + kAttnSplit - 1) / kAttnSplit) : 0;
+  const int ns = ok ? attn_nsplit(T + 1) : 0;
+  const int units = 2 * ns;
   io.arrive();
   if (blk >= units) return true;
   io.mark(0);   // trace: stage entry
   const int rrow = a.rope_row != nullptr ? ldc_i(a.rope_row) : T;
+  const bool lng = T + 1 > kAttnShortMax;
   for (int u = blk; u < units; u += nblk) {
     const int s = u >> 1, j = u & 1;
-    const bool done = T / kAttnSplit == s ? attn_unit<true>(a, s, j, T, rrow, io)
-                                          : attn_unit<false>(a, s, j, T, rrow, io);
+    const bool own = s == ns - 1;   // slot T lies in the last split
+    bool done;
+    if (lng)
+      done = own ? attn_unit_long<true>(a, s, j, T, rrow, io) : attn_unit_long<false>(a, s, j, T, rrow, io);
+    else
+      done = own ? attn_unit<true>(a, s, j, T, rrow, io) : attn_unit<false>(a, s, j, T, rrow, io);
     if (!done) return false;
   }
   return true;
@@ -2115,12 +2361,75 @@ __device__ __forceinline__ bool attn_body(const AttnArgs& a, int T, int blk, int
 // costs), then wave 0 folds them in split order, one dimension per lane.
 constexpr int kCombineWGs = 32;
 constexpr int kCombineChunk = 32;   // splits per LDS round (8 per wave)
+// Long contexts (at most kAttnMaxSplits splits up to 65536 positions): the
+// same workgroups, but wave w folds the contiguous quarter of the splits
+// [w c, (w + 1) c), c = ceil(ns / 4), in split order (L_w = L_w + l_s e_s,
+// ctx_w = ctx_w + acc_s e_s, e_s = exp(m_s - M), M the maximum over all
+// splits), and the quarters meet in LDS as (q0 + q1) + (q2 + q3).
+constexpr int kCombineLongPer = 32;   // splits per wave per round
+template <class IO>
+__device__ __forceinline__ bool combine_long(const AttnArgs& a, int T, int blk, IO& io) {
+  const int h = blk >> 2, q = blk & 3;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int d = 64 * q + lane;
+  const int ns = attn_nsplit(T + 1);
+  const int base = h * a.nsplit_max;
+  const int c = (ns + 3) / 4;
+  const int s0 = min(wave * c, ns), s1 = min(s0 + c, ns);
+  const Raw graw = io.issue1(a.qkv, h * 512 + 256 + d, wave == 0);   // the output gate of dimension d
+  float M = -__builtin_inff();   // over every split (each wave: the same value)
+  for (int b0 = 0; b0 < ns; b0 += 64) {
+    float mv;
+    if (!io.ld1(a.pm, a.part_st, base + min(b0 + lane, ns - 1), mv)) return false;
+    M = fmaxf(M, xor_max<64>(mv));
+  }
+  float L = 0.0f, ctx = 0.0f;
+  for (int r0 = s0; r0 < s1; r0 += kCombineLongPer) {
+    const int n = min(kCombineLongPer, s1 - r0);
+    int ia[kCombineLongPer];
+    float pa[kCombineLongPer];
+#pragma unroll
+    for (int k = 0; k < kCombineLongPer; ++k) ia[k] = (base + r0 + min(k, n - 1)) * 256 + d;
+    if (!io.template ldn<kCombineLongPer>(a.pacc, a.part_st, ia, pa)) return false;
+    float mv, lv;
+    const int sl = base + r0 + min(lane, n - 1);
+    if (!io.ld1(a.pm, a.part_st, sl, mv) || !io.ld1(a.pl, a.part_st, sl, lv)) return false;
+    const float e = dev_expf(mv - M);   // split r0 + lane
+#pragma unroll
+    for (int k = 0; k < kCombineLongPer; ++k) {
+      if (k < n) {
+        const float ek = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), k));
+        const float lk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lv), k));
+        L = L + lk * ek;
+        ctx = ctx + pa[k] * ek;
+      }
+    }
+  }
+  float* buf = io.slot();   // [4 waves]: L at 0, ctx at 4 + 64 w
+  as_lds_w(buf)[4 + 64 * wave + lane] = ctx;
+  if (lane == 0) as_lds_w(buf)[wave] = L;
+  lds_barrier();
+  if (wave != 0) {
+    settle(graw.v), settle(graw.t);
+    return true;
+  }
+  const float Ls = (as_lds(buf)[0] + as_lds(buf)[1]) + (as_lds(buf)[2] + as_lds(buf)[3]);
+  const float cs = (as_lds(buf)[4 + lane] + as_lds(buf)[68 + lane]) + (as_lds(buf)[132 + lane] + as_lds(buf)[196 + lane]);
+  io.mark(1);   // trace: all split partials folded
+  const float invL = 1.0f / Ls;
+  float gate;
+  if (!io.resolve1(graw, a.qkv, a.qkv_st, h * 512 + 256 + d, gate)) return false;
+  io.st1(a.og, a.og_st, h * 256 + d, (cs * invL) * dev_sigmoid(gate));
+  return true;
+}
+
 template <class IO>
 __device__ __forceinline__ bool combine_body(const AttnArgs& a, int T, int blk, IO& io) {
   io.arrive();
   io.mark(0);   // trace: stage entry
   if (!io.wait()) return false;
   if (blk >= kCombineWGs || T < 0 || T >= a.max_ctx) return true;
+  if (T + 1 > kAttnShortMax) return combine_long(a, T, blk, io);
   const int h = blk >> 2, q = blk & 3;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int d = 64 * q + lane;

@@ -99,6 +99,31 @@ def test_persistent_equals_graph_path(q, engine, mode):
     assert gen_p == gen_g and pos_p == pos_g == 23
 
 
+def test_persistent_equals_graph_path_long_context(q, blob):
+    """Past 2048 cached positions the attention stages switch to the long-context splits: both
+    executors, W8A8, an 8-token prompt then greedy decoding to 2078 positions, give the same
+    tokens, the same K/V cache rows and the same logits at the last step."""
+    n = 2080
+    e = q.Engine(blob, max_ctx=n, mode=q.MODE_W8A8)
+    try:
+        runs = []
+        for ex in (q.EXEC_GRAPH, q.EXEC_PERSISTENT):
+            e.set_exec(ex)
+            e.reset()
+            gen = e.generate([11, 2222, 33333, 4, 5, 6, 7, 8], 2069)
+            am, lg = e.decode_token(gen[-1], want_logits=True)
+            runs.append((gen, am, lg, e.pos, d2h(e.device_ptr(3), (6, n, 512)), d2h(e.device_ptr(4), (6, n, 512))))
+            assert e.exec_kind == ex
+        (gen_g, am_g, lg_g, pos_g, k_g, v_g), (gen_p, am_p, lg_p, pos_p, k_p, v_p) = runs
+        assert pos_g == pos_p == 2078
+        assert gen_p == gen_g and am_p == am_g
+        assert_bitwise(lg_p, lg_g, "logits at position 2078")
+        assert_bitwise(k_p[:, :pos_p], k_g[:, :pos_g], "k cache")
+        assert_bitwise(v_p[:, :pos_p], v_g[:, :pos_g], "v cache")
+    finally:
+        e.close()
+
+
 def test_reset_restarts_the_sequence(engine):
     engine.set_mode(0)
     engine.reset()

@@ -132,9 +132,12 @@ def test_attention_layer(q, orc, W, w8a8, Tpast):
         assert_close_norm(out_d.cpu().numpy(), o2, 1e-4, what="attention vs reference order")
 
 
-@pytest.mark.parametrize("T", [511, 4095, 32767])
-def test_attention_long_context(q, orc, W, T):
-    """C3: KV cache ~ N(0,1) at context 512 / 4096 / 32768 (the reference's sc[8192] bound does not apply)."""
+@pytest.mark.parametrize("T,w8a8", [(511, False), (2060, False), (4095, False), (4095, True), (32767, False)],
+                         ids=["512", "2061-last-split-of-one", "4096", "4096-w8a8", "32768"])
+def test_attention_long_context(q, orc, W, T, w8a8):
+    """C3: KV cache ~ N(0,1) at context 512 / 4096 / 32768 (the reference's sc[8192] bound does not apply).
+    Above 2048 positions the splits are longer (4 ceil(Tn / 512) positions) and the four waves of a unit
+    share them; at Tn = 2061 the last split holds one position, so three of its waves have none."""
     torch = W.torch
     pre = "layers.3.self_attn."
     r = rng(T)
@@ -142,14 +145,16 @@ def test_attention_long_context(q, orc, W, T):
     kc = f32(r.standard_normal((T + 1, 512)))
     vc = f32(r.standard_normal((T + 1, 512)))
     out_d, kc_d, vc_d = torch.empty(1024, device="cuda"), W.up(kc), W.up(vc)
-    q.attention_layer(out_d, W.up(x), *_attn_args(q, W, pre), T, kc_d, vc_d, T)
+    q.attention_layer(out_d, W.up(x), *_attn_args(q, W, pre), T, kc_d, vc_d, T, w8a8=w8a8)
     torch.cuda.synchronize()
     o1, k1, v1 = np.empty(1024, np.float32), kc.copy(), vc.copy()
     orc.lib().or_attention_layer(p(o1), p(x), W.ot[pre + "q_proj.weight"], W.ot[pre + "k_proj.weight"],
                                  W.ot[pre + "v_proj.weight"], W.ot[pre + "o_proj.weight"],
                                  p(W.host(pre + "q_norm.weight")[0]), p(W.host(pre + "k_norm.weight")[0]), T,
-                                 p(k1), p(v1), T, orc.W8A16, orc.ORDER_DEV)
+                                 p(k1), p(v1), T, orc.W8A8 if w8a8 else orc.W8A16, orc.ORDER_DEV)
     assert_bitwise(out_d.cpu().numpy(), o1, f"attention T={T} vs twin")
+    assert_bitwise(kc_d.cpu().numpy().reshape(T + 1, 512), k1, f"k cache T={T}")
+    assert_bitwise(vc_d.cpu().numpy().reshape(T + 1, 512), v1, f"v cache T={T}")
 
 
 @pytest.mark.parametrize("w8a8", [False, True])
