@@ -128,6 +128,17 @@ int qh_delta_rule_head(const float* q, const float* k, const float* v, float g, 
  *                                                            deltanet.hpp:118-127 delta_rule_layer */
 int qh_delta_rule_layer(const float* q, const float* k, const float* v, const float* g,
                         const float* beta, float* S, float* out, void* stream);
+/* the DeltaNet recurrent step between the projections       deltanet.hpp:154-179 (inside deltanet_layer)
+ * short conv + SiLU over the projected qkv [6144] (conv_state [6144][4] and
+ * rec [16][128][128] updated in place), beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias),
+ * l2norm of q and k, q / sqrt(128), the delta rule, per-head gated RMSNorm with silu(z [2048]):
+ * out [2048] (the input of out_proj).  The reference has no separate entry for this step; it is
+ * the body of deltanet_layer.  Scratch comes from the caller: workspace, 256-byte aligned, at least
+ * qh_deltanet_step_workspace() bytes (nothing is allocated). */
+size_t qh_deltanet_step_workspace(void);
+int qh_deltanet_step(float* out, const float* qkv, const float* z, const float* b, const float* a,
+                     const float* conv_w, const float* A_log, const float* dt_bias, const float* gate_norm_w,
+                     float* rec, float* conv_state, void* workspace, size_t workspace_bytes, void* stream);
 /* full Gated DeltaNet decode step, x already input-normed    deltanet.hpp:141-182 deltanet_layer
  * rec[16][128][128] and conv_state[6144][4] are updated in place. */
 int qh_deltanet_layer(float* out, const float* x, const qh_tensor* qkv_w, const qh_tensor* z_w,

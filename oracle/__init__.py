@@ -99,6 +99,7 @@ def lib():
         _sig(L, "or_gemv_w8a8", None, [P, P, P, P, P, F, I, I])
         _sig(L, "or_gemv_acc_i64", None, [P, P, P, I, I])
         _sig(L, "or_deltanet_layer", None, [P, P, T, T, T, T, P, P, P, P, T, P, P, I, I])
+        _sig(L, "or_deltanet_step", None, [P, P, P, P, P, P, P, P, P, P, P, I])
         _sig(L, "or_attention_layer", None, [P, P, T, T, T, T, P, P, I, P, P, I, I, I])
         _sig(L, "or_mlp_layer", None, [P, P, T, T, T, I, I])
         _sig(L, "or_model_new", P, [P, ctypes.c_char_p, I])

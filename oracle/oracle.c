@@ -564,20 +564,13 @@ static void proj_f32(float* y, const or_tensor* t, const act_t* a, int mode, int
  * Layer ops (deltanet.hpp:141-182, attention.hpp:25-95, mlp.hpp:11-19) with
  * the W8A8 quantization points of golden/model.py.
  * ================================================================== */
-void or_deltanet_layer(float* out, const float* x, const or_tensor* qkv_w, const or_tensor* z_w,
-                       const or_tensor* b_w, const or_tensor* a_w, const float* conv_w,
-                       const float* A_log, const float* dt_bias, const float* gate_norm_w,
-                       const or_tensor* out_w, float* rec, float* conv_state, int mode, int order) {
-  float qkv[CONV_DIM], z[Z_DIM], b[LH], a[LH], convd[CONV_DIM];
-  float q[LH * LK], k[LH * LK], v[LH * LV], g[LH], beta[LH], o[LH * LV], og[VALUE_DIM];
-  int8_t qbuf[VALUE_DIM];
-  float xfbuf[VALUE_DIM];
-  act_t act;
-  act_prepare(&act, x, HIDDEN, mode, qbuf, xfbuf);   /* model.py:143 xq = _qa(x) */
-  proj_i8(qkv, qkv_w, &act, mode, order);
-  proj_i8(z, z_w, &act, mode, order);
-  proj_f32(b, b_w, &act, mode, order);
-  proj_f32(a, a_w, &act, mode, order);
+/* The recurrent step between the projections (deltanet.hpp:154-179): short conv + SiLU over the
+ * qkv stream, gates, l2norm, delta rule, per-head gated RMSNorm into og[VALUE_DIM]. */
+static void deltanet_core(float* og, const float* qkv, const float* z, const float* b, const float* a,
+                          const float* conv_w, const float* A_log, const float* dt_bias,
+                          const float* gate_norm_w, float* rec, float* conv_state, int mode, int order) {
+  float convd[CONV_DIM];
+  float q[LH * LK], k[LH * LK], v[LH * LV], g[LH], beta[LH], o[LH * LV];
   conv1d_step_o(convd, qkv, conv_state, conv_w, order);
   for (int h = 0; h < LH; ++h) {   /* deltanet.hpp:160-170 */
     for (int i = 0; i < LK; ++i) q[h * LK + i] = convd[h * LK + i];
@@ -600,6 +593,28 @@ void or_deltanet_layer(float* out, const float* x, const or_tensor* qkv_w, const
   }
   for (int h = 0; h < LH; ++h)   /* deltanet.hpp:177-179 */
     gemv_rmsnorm_gated_o(og + h * LV, o + h * LV, gate_norm_w, z + h * LV, LV, EPS, mode, order);
+}
+
+void or_deltanet_step(float* og, const float* qkv, const float* z, const float* b, const float* a,
+                      const float* conv_w, const float* A_log, const float* dt_bias, const float* gate_norm_w,
+                      float* rec, float* conv_state, int order) {
+  deltanet_core(og, qkv, z, b, a, conv_w, A_log, dt_bias, gate_norm_w, rec, conv_state, OR_W8A16, order);
+}
+
+void or_deltanet_layer(float* out, const float* x, const or_tensor* qkv_w, const or_tensor* z_w,
+                       const or_tensor* b_w, const or_tensor* a_w, const float* conv_w,
+                       const float* A_log, const float* dt_bias, const float* gate_norm_w,
+                       const or_tensor* out_w, float* rec, float* conv_state, int mode, int order) {
+  float qkv[CONV_DIM], z[Z_DIM], b[LH], a[LH], og[VALUE_DIM];
+  int8_t qbuf[VALUE_DIM];
+  float xfbuf[VALUE_DIM];
+  act_t act;
+  act_prepare(&act, x, HIDDEN, mode, qbuf, xfbuf);   /* model.py:143 xq = _qa(x) */
+  proj_i8(qkv, qkv_w, &act, mode, order);
+  proj_i8(z, z_w, &act, mode, order);
+  proj_f32(b, b_w, &act, mode, order);
+  proj_f32(a, a_w, &act, mode, order);
+  deltanet_core(og, qkv, z, b, a, conv_w, A_log, dt_bias, gate_norm_w, rec, conv_state, mode, order);
   act_t act2;
   act_prepare(&act2, og, VALUE_DIM, mode, qbuf, xfbuf);   /* model.py:191 _qa(o) */
   proj_i8(out, out_w, &act2, mode, order);

@@ -98,6 +98,11 @@ void or_gemv_w8a8(float* y, int32_t* acc, const int8_t* w, const float* sw, cons
 void or_gemv_acc_i64(int64_t* acc, const int8_t* w, const int8_t* xq, int out, int in);
 
 /* ---- layer ops (mode OR_W8A16 / OR_W8A8, order REF / DEV) ---- */
+/* BASELINE config C2: the recurrent step between the projections (deltanet.hpp:154-179) on the
+ * projected qkv [6144], z [2048], b [16], a [16]; og = the gated-normed heads [2048] (fp32 order). */
+void or_deltanet_step(float* og, const float* qkv, const float* z, const float* b, const float* a,
+                      const float* conv_w, const float* A_log, const float* dt_bias, const float* gate_norm_w,
+                      float* rec, float* conv_state, int order);
 void or_deltanet_layer(float* out, const float* x, const or_tensor* qkv_w, const or_tensor* z_w,
                        const or_tensor* b_w, const or_tensor* a_w, const float* conv_w,
                        const float* A_log, const float* dt_bias, const float* gate_norm_w,

@@ -267,6 +267,32 @@ def delta_rule_layer(q, k, v, g, beta, S, out, stream=None):
           _dev(out, "f32", 2048, "out"), _Ptr(_stream(stream)))
 
 
+def deltanet_step_workspace() -> int:
+    """Bytes of device scratch qh_deltanet_step takes from its caller."""
+    f = _lib().qh_deltanet_step_workspace
+    f.restype = ctypes.c_size_t
+    return int(f())
+
+
+def deltanet_step(out, qkv, z, b, a, conv_w, A_log, dt_bias, gate_norm_w, rec, conv_state, workspace,
+                  stream=None):
+    """The DeltaNet recurrent step between the projections (deltanet.hpp:154-179; config C2):
+    conv + SiLU, gates, l2norm, delta rule, per-head gated RMSNorm.  `workspace` is a device
+    tensor of at least deltanet_step_workspace() bytes (256-byte aligned); nothing is allocated."""
+    if not getattr(workspace, "is_cuda", False) or not workspace.is_contiguous():
+        raise TypeError("workspace: a contiguous tensor on the GPU")
+    nbytes = workspace.numel() * workspace.element_size()
+    fn = _lib().qh_deltanet_step
+    _check(fn(*[ctypes.c_void_p(_ptr(t)) for t in (
+        _dev(out, "f32", 2048, "out"), _dev(qkv, "f32", CONV_DIM, "qkv"), _dev(z, "f32", 2048, "z"),
+        _dev(b, "f32", 16, "b"), _dev(a, "f32", 16, "a"), _dev(conv_w, "f32", CONV_DIM * 4, "conv_w"),
+        _dev(A_log, "f32", 16, "A_log"), _dev(dt_bias, "f32", 16, "dt_bias"),
+        _dev(gate_norm_w, "f32", 128, "gate_norm_w"), _dev(rec, "f32", 16 * 128 * 128, "rec"),
+        _dev(conv_state, "f32", CONV_DIM * 4, "conv_state"), workspace)],
+        ctypes.c_size_t(nbytes), ctypes.c_void_p(_stream(stream) or 0) if _stream(stream) else None),
+        "qh_deltanet_step")
+
+
 def deltanet_layer(out, x, qkv_w: Tensor, z_w: Tensor, b_w: Tensor, a_w: Tensor, conv_w, A_log, dt_bias,
                    gate_norm_w, out_w: Tensor, rec, conv_state, w8a8: bool = False, stream=None):
     _call("qh_deltanet_layer_w8a8" if w8a8 else "qh_deltanet_layer", _dev(out, "f32", HIDDEN, "out"),

@@ -4,6 +4,7 @@
 // in qh_device.hpp, so results do not depend on grid size or timing.
 #include <hip/hip_ext.h>
 
+#include "qh_decode.h"
 #include "qh_stages.hpp"
 
 namespace qh {
@@ -186,9 +187,13 @@ hipError_t launch_embed(float* h, const int8_t* w, const float* sc, int tok, int
 }
 
 // one wave: C16 sum of squares over n, then the (1+w) or gated scaling.
+// One vector of n per workgroup: workgroup b normalises x[b n .. b n + n) (w shared).
 __global__ void rmsnorm_kernel(float* y, const float* x, const float* w, const float* z, int n, float eps,
                                int gated) {
   const int lane = threadIdx.x;
+  y += (size_t)blockIdx.x * n;
+  x += (size_t)blockIdx.x * n;
+  if (z != nullptr) z += (size_t)blockIdx.x * n;
   const int nchunk = (n + 15) / 16;
   float ss = 0.0f;
   for (int c = lane; c < nchunk; c += 64)
@@ -202,8 +207,8 @@ __global__ void rmsnorm_kernel(float* y, const float* x, const float* w, const f
     }
 }
 hipError_t launch_rmsnorm(float* y, const float* x, const float* w, const float* z, int n, float eps,
-                          int gated, hipStream_t s) {
-  rmsnorm_kernel<<<1, 64, 0, s>>>(y, x, w, z, n, eps, gated);
+                          int gated, hipStream_t s, int groups) {
+  rmsnorm_kernel<<<groups, 64, 0, s>>>(y, x, w, z, n, eps, gated);
   return hipGetLastError();
 }
 
@@ -223,9 +228,8 @@ hipError_t launch_l2norm(float* v, int n, hipStream_t s) {
   return hipGetLastError();
 }
 
-__global__ void conv1d_kernel(float* out, const float* in, float* state, const float* w, int C) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= C) return;
+// conv1d_step + SiLU of channel c (conv1d.hpp): state [C][4], weight [C][4]
+__device__ __forceinline__ void conv1d_channel(float* out, const float* in, float* state, const float* w, int c) {
   float* st = state + (size_t)c * 4;
   const float* wc = w + (size_t)c * 4;
   const float w0 = st[1], w1 = st[2], w2 = st[3], w3 = in[c];
@@ -239,6 +243,30 @@ __global__ void conv1d_kernel(float* out, const float* in, float* state, const f
   st[2] = w2;
   st[3] = w3;
   out[c] = dev_silu(acc);
+}
+__global__ void conv1d_kernel(float* out, const float* in, float* state, const float* w, int C) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c < C) conv1d_channel(out, in, state, w, c);
+}
+// The DeltaNet step's inputs of the delta rule (deltanet.hpp:155-165): the short conv + SiLU of
+// the 6144 qkv channels, and per head beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias)
+// into gb = g[16] | beta[16] (threads 6144 .. 6159).
+__global__ void dn_step_pre_kernel(float* convd, float* gb, const float* qkv, float* state, const float* cw,
+                                   const float* b, const float* a, const float* A_log, const float* dt_bias) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c < QH_CONV_DIM) {
+    conv1d_channel(convd, qkv, state, cw, c);
+  } else if (c < QH_CONV_DIM + QH_LH) {
+    const int h = c - QH_CONV_DIM;
+    gb[QH_LH + h] = dev_sigmoid(b[h]);
+    gb[h] = -dev_expf(A_log[h]) * dev_softplus(a[h] + dt_bias[h]);
+  }
+}
+hipError_t launch_dn_step_pre(float* convd, float* gb, const float* qkv, float* state, const float* cw,
+                              const float* b, const float* a, const float* A_log, const float* dt_bias,
+                              hipStream_t s) {
+  dn_step_pre_kernel<<<(QH_CONV_DIM + QH_LH + 255) / 256, 256, 0, s>>>(convd, gb, qkv, state, cw, b, a, A_log, dt_bias);
+  return hipGetLastError();
 }
 hipError_t launch_conv1d(float* out, const float* in, float* state, const float* w, int C, hipStream_t s) {
   conv1d_kernel<<<(C + 255) / 256, 256, 0, s>>>(out, in, state, w, C);

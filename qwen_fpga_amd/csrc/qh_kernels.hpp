@@ -272,8 +272,12 @@ hipError_t launch_advance(StepCtl* ctl, const int* prompt, int* out_ids, hipStre
 // small op kernels
 hipError_t launch_embed(float* h, const int8_t* w, const float* sc, int tok, int in, hipStream_t s);
 hipError_t launch_rmsnorm(float* y, const float* x, const float* w, const float* z, int n, float eps,
-                          int gated, hipStream_t s);
+                          int gated, hipStream_t s,
+                          int groups = 1);
 hipError_t launch_l2norm(float* v, int n, hipStream_t s);
+hipError_t launch_dn_step_pre(float* convd, float* gb, const float* qkv, float* state, const float* cw,
+                              const float* b, const float* a, const float* A_log, const float* dt_bias,
+                              hipStream_t s);
 hipError_t launch_conv1d(float* out, const float* in, float* state, const float* w, int C,
                          hipStream_t s);
 hipError_t launch_apply_rope(float* x, const float* cs, const float* sn, hipStream_t s);

@@ -453,6 +453,34 @@ int qh_delta_rule_layer(const float* q, const float* k, const float* v, const fl
   return hip_status(launch_deltanet(d, s));
 }
 
+// The scratch of qh_deltanet_step: post-conv qkv, g | beta, the delta-rule output.
+constexpr size_t kDnStepWorkspace = rnd(4 * kConvDim) + rnd(4 * 2 * kLH) + rnd(4 * kLH * kLV);
+size_t qh_deltanet_step_workspace(void) { return kDnStepWorkspace; }
+
+int qh_deltanet_step(float* out, const float* qkv, const float* z, const float* b, const float* a,
+                     const float* conv_w, const float* A_log, const float* dt_bias, const float* gate_norm_w,
+                     float* rec, float* conv_state, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!out || !qkv || !z || !b || !a || !conv_w || !A_log || !dt_bias || !gate_norm_w || !rec || !conv_state ||
+      !workspace)
+    return QH_EINVAL;
+  if (workspace_bytes < kDnStepWorkspace || (reinterpret_cast<uintptr_t>(workspace) & 255)) return QH_EINVAL;
+  hipStream_t s = S(stream);
+  Scratch sc(s, static_cast<char*>(workspace), workspace_bytes);
+  float* convd = sc.take<float>(kConvDim);
+  float* gb = sc.take<float>(2 * kLH);
+  float* o = sc.take<float>(kLH * kLV);
+  QH_HIP(launch_dn_step_pre(convd, gb, qkv, conv_state, conv_w, b, a, A_log, dt_bias, s));
+  DnArgs d;   // l2norm, q scale, delta rule (deltanet.hpp:166-175)
+  d.convd = convd;
+  d.gb = gb;
+  d.S = rec;
+  d.o = o;
+  d.heads = kLH;
+  QH_HIP(launch_deltanet(d, s));
+  // per-head gated RMSNorm with silu(z) (deltanet.hpp:177-179)
+  return hip_status(launch_rmsnorm(out, o, gate_norm_w, z, kLV, kEps, 1, s, kLH));
+}
+
 int qh_deltanet_layer(float* out, const float* x, const qh_tensor* qkv_w, const qh_tensor* z_w,
                       const qh_tensor* b_w, const qh_tensor* a_w, const float* conv_w, const float* A_log,
                       const float* dt_bias, const float* gate_norm_w, const qh_tensor* out_w, float* rec,

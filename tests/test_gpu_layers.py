@@ -95,6 +95,41 @@ def test_deltanet_layer(q, orc, W, w8a8):
         assert_close_norm(rec_d.cpu().numpy(), r2, 1e-4, what="rec vs reference order")
 
 
+def test_deltanet_step(q, orc, W):
+    """C2: the DeltaNet recurrent step between the projections (conv + SiLU, gates, l2norm, delta
+    rule, gated RMSNorm) on projected inputs ~ N(0, 1), three steps in a row on a warm state, with the
+    scratch from a caller workspace: output, recurrent state and conv state bit for bit equal to the
+    device twin, and close to the reference order."""
+    torch = W.torch
+    pre = "layers.0.linear_attn."
+    r = rng(62)
+    rec0 = f32(r.standard_normal((16, 128, 128)) * 0.05)
+    conv0 = f32(r.standard_normal((6144, 4)))
+    rec_d, conv_d = W.up(rec0), W.up(conv0)
+    r1, c1, r2, c2 = rec0.copy(), conv0.copy(), rec0.copy(), conv0.copy()
+    ws = torch.empty(q.deltanet_step_workspace(), dtype=torch.uint8, device="cuda")
+    host = [W.host(pre + n)[0] for n in ("conv1d.weight", "A_log", "dt_bias", "norm.weight")]
+    dev = [W.dev[pre + n][0] for n in ("conv1d.weight", "A_log", "dt_bias", "norm.weight")]
+    for step in range(3):
+        qkv, z = f32(r.standard_normal(6144)), f32(r.standard_normal(2048))
+        b, a = f32(r.standard_normal(16)), f32(r.standard_normal(16))
+        out_d = torch.empty(2048, device="cuda")
+        q.deltanet_step(out_d, W.up(qkv), W.up(z), W.up(b), W.up(a), *dev, rec_d, conv_d, ws)
+        torch.cuda.synchronize()
+        o1, o2 = np.empty(2048, np.float32), np.empty(2048, np.float32)
+        orc.lib().or_deltanet_step(p(o1), p(qkv), p(z), p(b), p(a), *[p(h) for h in host], p(r1), p(c1),
+                                   orc.ORDER_DEV)
+        orc.lib().or_deltanet_step(p(o2), p(qkv), p(z), p(b), p(a), *[p(h) for h in host], p(r2), p(c2),
+                                   orc.ORDER_REF)
+        assert_bitwise(out_d.cpu().numpy(), o1, f"step {step} out vs twin")
+        assert_bitwise(rec_d.cpu().numpy(), r1, f"step {step} rec vs twin")
+        assert_bitwise(conv_d.cpu().numpy(), c1, f"step {step} conv vs twin")
+        assert_close_norm(out_d.cpu().numpy(), o2, 1e-4, what=f"step {step} out vs reference order")
+    with pytest.raises(q.QHError) as ex:   # a workspace below the size the op needs is refused
+        q.deltanet_step(out_d, W.up(qkv), W.up(z), W.up(b), W.up(a), *dev, rec_d, conv_d, ws[:1024])
+    assert ex.value.status == q.QH_EINVAL
+
+
 def _attn_args(q, W, pre):
     return (qt(q, W, pre + "q_proj.weight"), qt(q, W, pre + "k_proj.weight"), qt(q, W, pre + "v_proj.weight"),
             qt(q, W, pre + "o_proj.weight"), W.dev[pre + "q_norm.weight"][0], W.dev[pre + "k_norm.weight"][0])
