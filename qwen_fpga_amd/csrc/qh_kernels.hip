@@ -200,11 +200,8 @@ __global__ void rmsnorm_kernel(float* y, const float* x, const float* w, const f
     for (int e = 0; e < 16 && 16 * c + e < n; ++e) ss = __builtin_fmaf(x[16 * c + e], x[16 * c + e], ss);
   ss = xor_sum<64>(ss);
   const float inv = 1.0f / sqrtf(ss / (float)n + eps);
-  for (int c = lane; c < nchunk; c += 64)
-    for (int e = 0; e < 16 && 16 * c + e < n; ++e) {
-      const int i = 16 * c + e;
-      y[i] = gated ? ((x[i] * inv) * w[i]) * dev_silu(z[i]) : (x[i] * inv) * (1.0f + w[i]);
-    }
+  for (int i = lane; i < n; i += 64)   // elementwise: any lane order
+    y[i] = gated ? ((x[i] * inv) * w[i]) * dev_silu(z[i]) : (x[i] * inv) * (1.0f + w[i]);
 }
 hipError_t launch_rmsnorm(float* y, const float* x, const float* w, const float* z, int n, float eps,
                           int gated, hipStream_t s, int groups) {

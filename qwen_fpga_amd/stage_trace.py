@@ -83,6 +83,19 @@ def summarise(path: str, token: int = 1) -> list:
     return rows
 
 
+def span_us(path: str, token: int = 1, last_stage: int = -1) -> float:
+    """Microseconds from the end of token `token` - 1 (its last stage, on the workgroup that
+    finished it last) to the end of stage `last_stage` of token `token`, on the kernel's clock."""
+    d = np.loadtxt(path, dtype=np.float64, comments="#", ndmin=2)
+    tok, st = d[:, 0].astype(int), d[:, 1].astype(int)
+    end = d[:, -1]
+    ns = st.max() + 1
+    last = last_stage % ns
+    t1 = end[(tok == token) & (st == last)].max()
+    t0 = end[(tok == token - 1) & (st == ns - 1)].max()
+    return (t1 - t0) * TICK_US
+
+
 def main(argv=None) -> None:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--pos", type=int, default=305)
