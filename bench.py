@@ -489,8 +489,125 @@ def cpu_baseline(blob, idx, prompt, ntok, act_mode):
                      "sample": f"{ntok} decode tokens from a fresh state, the reference hls/src qwen_top compiled "
                                f"-O2 -ffp-contract=off (csim build; w8a16)"})
     out = dict(legs[0])
-    out["legs"] = legs[1:]
+    out["legs"] = legs[1:] + cpu_config_legs(blob, idx)
     return out
+
+
+def cpu_config_legs(blob, idx):
+    """BASELINE.json configs C1-C4 on one core, per unit: the reference's hls/src kernels
+    (oracle/_ref, compiled from the headers where they lie) built -O3 (`value`) and with the
+    reference's csim flags, -O2 (`value_o2`), both -ffp-contract=off, W8A16 (the reference's own
+    arithmetic).  C3 at T = 32768 exceeds the reference's sc[8192] bound (attention.hpp:66): that
+    unit runs this repository's C restatement in the reference order (oracle.c, -O3, one thread).
+    Each unit is timed over a bounded sample (`calls`) after one untimed call."""
+    import numpy as np
+    import oracle
+    import qwen_fpga_amd as q
+    r3, r2 = oracle.ref(True), oracle.ref()
+    if r3 is None or r2 is None:
+        return []
+    P = lambda a: a.ctypes.data
+    rng = np.random.default_rng(3)
+    f32 = lambda *shape: np.ascontiguousarray(rng.standard_normal(shape).astype(np.float32))
+    entries = q.parse_idx(idx)
+
+    def tensor(name):
+        e = entries[name]
+        if e.dtype == 1:
+            w = blob[e.off:e.off + e.nbytes].view(np.int8).reshape(e.out, e.in_)
+            return oracle.tensor_i8(w, blob[e.soff:e.soff + e.snbytes].view(np.float32)), w
+        w = np.ascontiguousarray(blob[e.off:e.off + e.nbytes].view(np.float32))
+        return (oracle.tensor_f32(w.reshape(e.out, e.in_)) if e.in_ > 1 and e.out * e.in_ == w.size else None), w
+
+    def timed(fn, calls):
+        fn()
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            fn()
+        return (time.perf_counter() - t0) / calls * 1e6
+
+    def leg(cfg, unit_bytes, calls, f3, f2=None, kind="reference", flags="-O3 / -O2 (value_o2)"):
+        us3 = timed(f3, calls)
+        d = {"config": cfg, "value": round(us3, 1), "unit": "us per unit", "cores": 1, "kind": kind,
+             "bytes": int(unit_bytes), "gbs": round(unit_bytes / us3 / 1e3, 2), "calls": calls, "flags": flags}
+        if f2 is not None:
+            us2 = timed(f2, calls)
+            d["value_o2"] = round(us2, 1)
+        return d
+
+    legs = []
+    # C1: the reference gemv_i8 (gemv.hpp:28-42), int8 weights x fp32 activation, 4 rotating copies
+    for n, k in ((3584, 1024), (1024, 3584), (6144, 1024)):
+        W = [np.ascontiguousarray(q.synth_i8(n * k, 11 + n + c).reshape(n, k)) for c in range(4)]
+        sw = q.synth_uniform(n, 13 + n, 1e-3, 1e-2)
+        x, y = f32(k), np.empty(n, np.float32)
+        it = [0]
+
+        def mk(L):
+            def f():
+                it[0] += 1
+                L.ref_gemv_i8(P(y), P(W[it[0] % 4]), P(sw), P(x), n, k)
+            return f
+        legs.append(leg(f"C1 {n}x{k}", n * k + 4 * n + 4 * k + 4 * n, 120, mk(r3), mk(r2)))
+    # C2: the recurrent step from projected inputs (deltanet.hpp:154-179) on a warm state
+    pre = "layers.0.linear_attn."
+    cw, Al, dtb, nw = (tensor(pre + n)[1] for n in ("conv1d.weight", "A_log", "dt_bias", "norm.weight"))
+    qkv, z, b, a = f32(6144), f32(2048), f32(16), f32(16)
+    og = np.empty(2048, np.float32)
+    rec, cs = f32(16 * 128 * 128) * np.float32(0.05), f32(6144 * 4)
+
+    def step(L):
+        return lambda: L.ref_deltanet_step(P(og), P(qkv), P(z), P(b), P(a), P(cw), P(Al), P(dtb), P(nw), P(rec), P(cs))
+    legs.append(leg("C2", 2_384_640, 400, step(r3), step(r2)))
+    # C3: the attention layer (attention.hpp:25-95) over an N(0,1) cache of T past tokens
+    pa = "layers.3.self_attn."
+    at = [tensor(pa + n + "_proj.weight")[0] for n in ("q", "k", "v", "o")]
+    qn, kn = tensor(pa + "q_norm.weight")[1], tensor(pa + "k_norm.weight")[1]
+    xa, ya = f32(1024), np.empty(1024, np.float32)
+    for T, calls in ((512, 40), (4096, 12)):
+        kc, vc = f32((T + 1) * 512), f32((T + 1) * 512)
+
+        def att(L):
+            return lambda: L.ref_attention_layer(P(ya), P(xa), *at, P(qn), P(kn), T, P(kc), P(vc), T)
+        legs.append(leg(f"C3 T={T}", 7_364_608 + 2_048 + 4_096 * T + 4_096, calls, att(r3), att(r2)))
+    T = 32768
+    kc, vc = f32((T + 1) * 512), f32((T + 1) * 512)
+    import ctypes
+    os.environ["OMP_NUM_THREADS"] = "1"
+    L = oracle.lib()
+    try:   # one thread also if the OpenMP runtime started before this call
+        ctypes.CDLL("libgomp.so.1").omp_set_num_threads(1)
+    except OSError:
+        pass
+    legs.append(leg(f"C3 T={T}", 7_364_608 + 2_048 + 4_096 * T + 4_096, 2,
+                    lambda: L.or_attention_layer(P(ya), P(xa), *at, P(qn), P(kn), T, P(kc), P(vc), T, oracle.W8A16,
+                                                 oracle.ORDER_REF),
+                    kind="port", flags="oracle.c -O3 -ffp-contract=off, reference order (beyond the reference's sc[8192])"))
+    # C4: layers 0-3 (3 DeltaNet + 1 attention, each with its MLP) at T = 66 past tokens
+    states = {}
+
+    def block(Lr):
+        st = states.setdefault(id(Lr), {
+            "rec": [f32(16 * 128 * 128) * np.float32(0.05) for _ in range(3)], "conv": [f32(6144 * 4) for _ in range(3)],
+            "kc": f32(67 * 512), "vc": f32(67 * 512)})
+        h, t = f32(1024), np.empty(1024, np.float32)
+
+        def run():
+            for li in range(4):
+                if li < 3:
+                    pl = f"layers.{li}.linear_attn."
+                    args = [tensor(pl + n)[0] for n in ("in_proj_qkv.weight", "in_proj_z.weight", "in_proj_b.weight",
+                                                        "in_proj_a.weight")]
+                    ws = [tensor(pl + n)[1] for n in ("conv1d.weight", "A_log", "dt_bias", "norm.weight")]
+                    Lr.ref_deltanet_layer(P(t), P(h), *args, *[P(w) for w in ws], tensor(pl + "out_proj.weight")[0],
+                                          P(st["rec"][li]), P(st["conv"][li]))
+                else:
+                    Lr.ref_attention_layer(P(t), P(h), *at, P(qn), P(kn), 66, P(st["kc"]), P(st["vc"]), 66)
+                pm = f"layers.{li}.mlp."
+                Lr.ref_mlp_layer(P(h), P(t), *[tensor(pm + n + "_proj.weight")[0] for n in ("gate", "up", "down")])
+        return run
+    legs.append(leg("C4", 90_709_888 + 4_096 * 66, 8, block(r3), block(r2)))
+    return legs
 
 
 if __name__ == "__main__":

@@ -138,11 +138,25 @@ def matvec_fixed(w: np.ndarray, xq: np.ndarray, mult: np.ndarray, shift: int = 1
     return yq, acc
 
 
-def ref():
-    """The compiled reference kernels, or None if oracle/_ref was not built."""
-    global _REF
+_REF_O3 = None
+REF_O3_PATH = os.path.join(_HERE, "_ref", "libqref_o3.so")
+
+
+def ref(o3: bool = False):
+    """The compiled reference kernels (the reference's csim flags, -O2; with o3, the same
+    sources built -O3), or None if oracle/_ref was not built."""
+    global _REF, _REF_O3
+    if o3:
+        if _REF_O3 is None and os.path.exists(REF_O3_PATH):
+            _REF_O3 = _ref_sigs(ctypes.CDLL(REF_O3_PATH))
+        return _REF_O3
     if _REF is None and os.path.exists(REF_PATH):
-        L = ctypes.CDLL(REF_PATH)
+        _REF = _ref_sigs(ctypes.CDLL(REF_PATH))
+    return _REF
+
+
+def _ref_sigs(L):
+    if True:
         T = ctypes.POINTER(OrTensor)
         _sig(L, "ref_gemv_i8", None, [P, P, P, P, I, I])
         _sig(L, "ref_gemv_f32", None, [P, P, P, I, I])
@@ -171,8 +185,8 @@ def ref():
         _sig(L, "ref_state_vc", P, [P, I])
         _sig(L, "ref_qwen_top", I, [P, P, I, P])
         _sig(L, "ref_decode_token", I, [P, ctypes.c_char_p, P, I, P])
-        _REF = L
-    return _REF
+        _sig(L, "ref_deltanet_step", None, [P] * 11)
+    return L
 
 
 class Model:

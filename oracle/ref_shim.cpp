@@ -3,6 +3,7 @@
 // they lie (/root/reference/hls/src, passed with -I) into oracle/_ref/libqref.so,
 // with the reference's csim flags (hls/Makefile:14-15: -O2 -ffp-contract=off).
 // Used only to pin the C restatement in oracle.c and as the CPU baseline.
+#include <cmath>
 #include <cstdint>
 #include <cstring>
 #include <sstream>
@@ -52,6 +53,28 @@ void ref_conv1d_step(float* out, const float* in, float* state, const float* w) 
   conv1d_step(out, in, reinterpret_cast<float(*)[CONV_K]>(state), w);
 }
 void ref_rope_cos_sin(int pos, float* c, float* s) { rope_cos_sin(pos, c, s); }
+// The recurrent step between deltanet_layer's projections, from the
+// reference's own functions in deltanet_layer's order (deltanet.hpp:154-179): conv1d_step,
+// the gates, l2norm and q scaling, delta_rule_layer, per-head rmsnorm_gated.
+void ref_deltanet_step(float* og, const float* qkv, const float* z, const float* b, const float* a,
+                       const float* conv_w, const float* A_log, const float* dt_bias, const float* gate_norm_w,
+                       float* rec, float* conv_state) {
+  static float convd[CONV_DIM], q[H][K], k[H][K], v[H][V], g[H], beta[H], o[H][V];
+  conv1d_step(convd, qkv, reinterpret_cast<float(*)[CONV_K]>(conv_state), conv_w);
+  for (int h = 0; h < H; ++h) {
+    for (int i = 0; i < K; ++i) q[h][i] = convd[h * K + i];
+    for (int i = 0; i < K; ++i) k[h][i] = convd[VALUE_DIM + h * K + i];
+    for (int i = 0; i < V; ++i) v[h][i] = convd[2 * VALUE_DIM + h * V + i];
+    beta[h] = sigmoidf(b[h]);
+    g[h] = -std::exp(A_log[h]) * softplusf(a[h] + dt_bias[h]);
+    l2norm(q[h], K);
+    l2norm(k[h], K);
+    const float scale = 1.0f / std::sqrt(float(K));
+    for (int i = 0; i < K; ++i) q[h][i] *= scale;
+  }
+  delta_rule_layer(q, k, v, g, beta, reinterpret_cast<float(*)[K][V]>(rec), o);
+  for (int h = 0; h < H; ++h) rmsnorm_gated(&og[h * V], o[h], gate_norm_w, &z[h * V], V, EPS);
+}
 void ref_apply_rope(float* x, const float* c, const float* s) { apply_rope(x, c, s); }
 void ref_l2norm(float* v, int n) { l2norm(v, n); }
 void ref_delta_rule_head(const float* q, const float* k, const float* v, float g, float beta, float* S,

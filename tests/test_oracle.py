@@ -144,6 +144,35 @@ def test_delta_rule_bitexact(orc, ref):
     assert_bitwise(h1, h2, "head S")
 
 
+def test_deltanet_step_bitexact(orc, ref, blob, entries):
+    """or_deltanet_step (the C2 step between the projections) in the reference order equals the
+    reference's own functions run in deltanet_layer's order (oracle/_ref, deltanet.hpp:154-179),
+    over three steps on a warm state with layer 0's conv, gate and norm weights; the -O3 build of
+    the reference gives the same bits as its csim -O2 build."""
+    def w(name):
+        e = entries["layers.0.linear_attn." + name]
+        return np.ascontiguousarray(blob[e.off:e.off + e.nbytes].view(np.float32))
+    cw, A_log, dtb, nw = w("conv1d.weight"), w("A_log"), w("dt_bias"), w("norm.weight")
+    r = rng(71)
+    rec0, conv0 = f32(r.standard_normal((16, 128, 128)) * 0.05), f32(r.standard_normal((6144, 4)))
+    libs = [(orc.lib().or_deltanet_step, (orc.ORDER_REF,)), (ref.ref_deltanet_step, ())]
+    r3 = orc.ref(True)
+    if r3 is not None:
+        libs.append((r3.ref_deltanet_step, ()))
+    states = [(rec0.copy(), conv0.copy()) for _ in libs]
+    for step in range(3):
+        qkv, z, b, a = (f32(r.standard_normal(n)) for n in (6144, 2048, 16, 16))
+        outs = []
+        for (fn, extra), (rec, cs) in zip(libs, states):
+            og = np.empty(2048, np.float32)
+            fn(p(og), p(qkv), p(z), p(b), p(a), p(cw), p(A_log), p(dtb), p(nw), p(rec), p(cs), *extra)
+            outs.append(og)
+        for i in range(1, len(libs)):
+            assert_bitwise(outs[i], outs[0], f"step {step} out, build {i}")
+            assert_bitwise(states[i][0], states[0][0], f"step {step} rec, build {i}")
+            assert_bitwise(states[i][1], states[0][1], f"step {step} conv, build {i}")
+
+
 def _layer_tensors(orc, blob, entries, layer):
     def T(name):
         e = entries[f"layers.{layer}.{name}"]
