@@ -89,17 +89,6 @@ def dot_scale(qw: np.ndarray, sw: np.ndarray, x: np.ndarray) -> np.ndarray:
     return (np.abs(qw.astype(np.float64)) @ np.abs(np.asarray(x, np.float64))) * np.abs(sw.astype(np.float64))
 
 
-def swiglu_scale(gate, up, x):
-    """The dot-product error scale carried into act = silu(g) * u (mlp.hpp:14-17): a relative error
-    e of g and of u (each relative to its sum |terms|) moves act by e * (|silu'(g) u| S_g + |silu(g)| S_u)."""
-    (qg, sg), (qu, su) = gate, up
-    g = (qg.astype(np.float64) @ np.asarray(x, np.float64)) * sg.astype(np.float64)
-    u = (qu.astype(np.float64) @ np.asarray(x, np.float64)) * su.astype(np.float64)
-    sig = 1.0 / (1.0 + np.exp(-g))
-    dsilu = sig * (1.0 + g * (1.0 - sig))
-    return np.abs(dsilu * u) * dot_scale(qg, sg, x) + np.abs(g * sig) * dot_scale(qu, su, x)
-
-
 def assert_close_dot(got, exp, scale, rtol=RTOL, atol=ATOL, what=""):
     """|got - exp| <= atol + rtol * scale elementwise, scale = sum |w_k x_k| of each element."""
     g, e = np.asarray(got, np.float64), np.asarray(exp, np.float64)
@@ -111,6 +100,30 @@ def assert_close_dot(got, exp, scale, rtol=RTOL, atol=ATOL, what=""):
         raise AssertionError(f"{what}: {int(bad.sum())} of {g.size} outside atol {atol} + rtol {rtol} * sum|terms|; "
                              f"first at {i}: {g.flat[i]!r} vs {e.flat[i]!r} (limit {lim.flat[i]:.3e}); "
                              f"max err/limit {np.max(err / lim):.3f}")
+
+
+# W8A16 golden stage outputs at which the reference's own pair -- its hls/src kernels compiled with
+# its csim flags against the golden's BLAS -- exceeds rtol 1e-4 / atol 1e-5 elementwise on these
+# fixtures (tests/test_tolerance_spread.py): only these keep the sum |w x| bound.
+DOT_BOUND = {"dn_in_proj_z", "dn_out_proj", "at_q_proj", "ml_down_proj", "dn_out", "ml_out"}
+PRODUCT_STAGES = {"ml_qa1_in"}   # silu(gate) * up: two factors within rtol make a product within 2 rtol
+
+
+def assert_stage(got, exp, key, scale, what=""):
+    """A W8A16 stage output against the golden: the literal tolerance, twice it for a product of two
+    reductions, the sum |w x| bound (`scale`) only at DOT_BOUND stages."""
+    if key in DOT_BOUND:
+        assert_close_dot(got, exp, scale, what=what)
+        return
+    f = 2.0 if key in PRODUCT_STAGES else 1.0
+    g, e = np.asarray(got, np.float64).reshape(-1), np.asarray(exp, np.float64).reshape(-1)
+    err = np.abs(g - e)
+    lim = f * (ATOL + RTOL * np.abs(e))
+    bad = err > lim
+    if bad.any():
+        i = int(np.flatnonzero(bad)[0])
+        raise AssertionError(f"{what}: {int(bad.sum())} of {g.size} outside {f:g} x (atol {ATOL} + rtol {RTOL} |exp|); "
+                             f"first at {i}: {g[i]!r} vs {e[i]!r}; max err/limit {np.max(err / lim):.3f}")
 
 
 def fake_quant_weights(blob: np.ndarray, e):
