@@ -263,6 +263,10 @@ int qh_engine_set_exec(qh_engine* e, int exec);
 int qh_engine_get_exec(const qh_engine* e);
 /* Cooperative launches refused so far (each switched the engine to QH_EXEC_GRAPH). */
 int qh_engine_exec_fallbacks(const qh_engine* e);
+/* workgroups the LM head runs on under executor `exec` (its batches of 8 rows go to wave w of
+ * workgroup b as batch 4 b + w, + 4 * grid, ...); QH_ESTATE for the persistent executor when the
+ * device has no cooperative launch.  No counterpart in the reference (its head is one loop). */
+int qh_engine_head_grid(const qh_engine* e, int exec);
 /* Zero recurrent/conv state, empty KV cache, pos = 0 (state.hpp:24-34). */
 int qh_engine_reset(qh_engine* e);
 /* Decode one token (qwen_top): returns the argmax (ties -> lowest id) in

@@ -490,6 +490,13 @@ class Engine:
         """Cooperative launches refused so far (each switched the engine to EXEC_GRAPH)."""
         return int(_lib().qh_engine_exec_fallbacks(self._h))
 
+    def head_grid(self, exec_kind: int) -> int:
+        """Workgroups the LM head runs on under an executor (row batch 4 b + w on wave w of workgroup b)."""
+        r = _lib().qh_engine_head_grid(self._h, ctypes.c_int(exec_kind))
+        if r < 0:
+            raise QHError(r, "qh_engine_head_grid")
+        return r
+
     @property
     def pos(self) -> int:
         return int(_lib().qh_engine_pos(self._h))

@@ -811,6 +811,12 @@ int qh_engine_set_exec(qh_engine* e, int exec) {
 }
 
 int qh_engine_get_exec(const qh_engine* e) { return e ? e->exec : QH_EINVAL; }
+int qh_engine_head_grid(const qh_engine* e, int exec) {
+  if (!e || (exec != QH_EXEC_PERSISTENT && exec != QH_EXEC_GRAPH)) return QH_EINVAL;
+  if (exec == QH_EXEC_PERSISTENT) return e->persist_grid > 0 ? e->persist_grid : QH_ESTATE;
+  return e->head_grid;
+}
+
 int qh_engine_exec_fallbacks(const qh_engine* e) { return e ? e->fallbacks : QH_EINVAL; }
 
 int qh_engine_reset(qh_engine* e) {

@@ -259,11 +259,13 @@ def test_argmax_tie_lowest_index_wins(q, orc, blob, idx, torch_cuda, exec_kind):
     index wins.  Row a (the argmax) of the tied embedding is copied to a lower row in another
     workgroup's range (that row must now win) and, separately, to a higher one (a must stay)."""
     tok = 17
+    ex = q.EXEC_GRAPH if exec_kind == "graph" else q.EXEC_PERSISTENT
     e0 = q.Engine(blob, max_ctx=4)
     a, _ = e0.decode_token(tok)
+    grid = e0.head_grid(ex)
     e0.close()
     emb = q.parse_idx(idx)["embed_tokens.weight"]
-    stride = 256 * 4   # head batches of 8 rows, one per wave, over 256 workgroups of 4 waves
+    stride = grid * 4   # head batches of 8 rows, one per wave, over this executor's workgroups of 4 waves
 
     def blk_of(r):
         return ((r // 8) % stride) // 4
@@ -281,8 +283,9 @@ def test_argmax_tie_lowest_index_wins(q, orc, blob, idx, torch_cuda, exec_kind):
         assert lg_t[other] == lg_t[a] and am_t == want
         e = q.Engine(b, max_ctx=4)
         try:
-            e.set_exec(q.EXEC_GRAPH if exec_kind == "graph" else q.EXEC_PERSISTENT)
+            e.set_exec(ex)
             am, lg = e.decode_token(tok, want_logits=True)
+            assert e.exec_kind == ex
             assert lg[other] == lg[a], "tied rows must give identical logits"
             assert am == want, f"tie between {a} and {other}: argmax {am}, want {want}"
         finally:
