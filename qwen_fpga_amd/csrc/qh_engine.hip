@@ -524,6 +524,7 @@ int run_persist(qh_engine* e, int tok0, int n_prompt, int n_new, int eos, bool w
   a.abort_flag = e->abort_dev;
   a.poll_limit = e->poll_limit;
   a.dn_lds = e->dn_lds ? 1 : 0;
+  a.long_ctx = e->max_ctx > kAttnShortMax ? 1 : 0;
   QH_HIP(hipEventRecord(e->launch_ev[0], s));
   if (const hipError_t le = launch_persist(a, e->persist_grid, s); le != hipSuccess) {
     (void)hipGetLastError();

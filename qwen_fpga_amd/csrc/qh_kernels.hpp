@@ -251,6 +251,8 @@ struct PersistArgs {
   uint64_t* trace = nullptr;    // optional [trace_tokens][nstage][grid][kTraceSlots]: stage marks and end
   int trace_tokens = 0;
   int dn_lds = 0;               // DeltaNet stages keep S in LDS (their unit_base >= 0)
+  int long_ctx = 0;             // the cache holds more than kAttnShortMax positions: the kernel
+                                // instantiation with the long-context attention (else without it)
 };
 constexpr int kPersistThreads = 256;
 constexpr int kTraceSlots = 8;  // marks 0..6 of a stage body, then its completion time

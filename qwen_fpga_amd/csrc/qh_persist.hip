@@ -41,7 +41,7 @@ static_assert(sizeof(Stage) % 4 == 0 && kStageWords <= kPersistThreads, "one des
 // descriptor an exited wave did not copy.  The flag is double-buffered like
 // the descriptors: slot p is written before the barrier of a boundary and read
 // after it, and written again only two boundaries later.
-template <int MODE>
+template <int MODE, bool LONG>
 __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistArgs P) {
   __shared__ float s_bv[kPersistThreads / 64];
   __shared__ int s_bi[kPersistThreads / 64];
@@ -109,8 +109,8 @@ __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistA
             ok = gemv_body<4, MODE, P_LOAD, 1, QH_INTER, kEmResid>(st.g, blk, nblk, io, tok);
           break;
         case ST_DELTANET: ok = deltanet_all(st.d, blk, nblk, io, tok); break;
-        case ST_ATTN: ok = attn_body(st.at, pos, blk, nblk, io); break;
-        case ST_COMBINE: ok = combine_body(st.at, pos, blk, io); break;
+        case ST_ATTN: ok = attn_body<TagIO, LONG>(st.at, pos, blk, nblk, io); break;
+        case ST_COMBINE: ok = combine_body<TagIO, LONG>(st.at, pos, blk, io); break;
         default: ok = head_body(st.hd, blk, nblk, io, P.logits); break;
       }
       if (tr != nullptr && t == 0) tr[kTraceSlots - 1] = __builtin_amdgcn_s_memrealtime();
@@ -182,14 +182,16 @@ int persist_max_grid(int* grid) {
   if (hipGetDevice(&dev) != hipSuccess) return -1;
   if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
   if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess || !coop) return -1;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, persist_kernel<M_W8A16>, kPersistThreads, 0) !=
-      hipSuccess)
-    return -1;
-  int occ2 = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ2, persist_kernel<M_W8A8>, kPersistThreads, 0) !=
-      hipSuccess)
-    return -1;
-  occ = occ < occ2 ? occ : occ2;
+  const void* fns[] = {reinterpret_cast<const void*>(persist_kernel<M_W8A16, false>),
+                       reinterpret_cast<const void*>(persist_kernel<M_W8A8, false>),
+                       reinterpret_cast<const void*>(persist_kernel<M_W8A16, true>),
+                       reinterpret_cast<const void*>(persist_kernel<M_W8A8, true>)};
+  occ = 1 << 30;
+  for (const void* fn : fns) {
+    int o = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, fn, kPersistThreads, 0) != hipSuccess) return -1;
+    occ = o < occ ? o : occ;
+  }
   if (occ < 1) return -1;
   int g = ncu < 256 ? ncu : 256;   // one workgroup per CU
   g -= g & 1;                      // the head partials are copied as pairs
@@ -201,8 +203,10 @@ int persist_max_grid(int* grid) {
 hipError_t launch_persist(const PersistArgs& a, int grid, hipStream_t s) {
   if (grid < 1 || grid > 256) return hipErrorInvalidValue;
   void* args[] = {const_cast<PersistArgs*>(&a)};
-  const void* fn = a.mode == M_W8A8 ? reinterpret_cast<const void*>(persist_kernel<M_W8A8>)
-                                    : reinterpret_cast<const void*>(persist_kernel<M_W8A16>);
+  const void* fn = a.long_ctx ? (a.mode == M_W8A8 ? reinterpret_cast<const void*>(persist_kernel<M_W8A8, true>)
+                                                   : reinterpret_cast<const void*>(persist_kernel<M_W8A16, true>))
+                             : (a.mode == M_W8A8 ? reinterpret_cast<const void*>(persist_kernel<M_W8A8, false>)
+                                                 : reinterpret_cast<const void*>(persist_kernel<M_W8A16, false>));
   return hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kPersistThreads), args, 0, s);
 }
 

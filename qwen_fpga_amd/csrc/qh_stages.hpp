@@ -2331,24 +2331,29 @@ __device__ __forceinline__ bool attn_unit_long(const AttnArgs& a, int s, int j, 
 
 // Units u = blk, blk + nblk, ... of the 2 * ceil((T+1)/16) splits; T is the slot
 // of this token (past tokens = T).
-template <class IO>
+// LONG = false leaves the long-context unit out of a kernel whose cache never holds more than
+// kAttnShortMax positions (its registers would otherwise weigh on the whole kernel); such a kernel
+// refuses a longer context (false: the launch's failure path).
+template <class IO, bool LONG = true>
 __device__ __forceinline__ bool attn_body(const AttnArgs& a, int T, int blk, int nblk, IO& io) {
   const bool ok = T >= 0 && T < a.max_ctx;
   const int ns = ok ? attn_nsplit(T + 1) : 0;
   const int units = 2 * ns;
   io.arrive();
+  if (!LONG && T + 1 > kAttnShortMax) return false;
   if (blk >= units) return true;
   io.mark(0);   // trace: stage entry
   const int rrow = a.rope_row != nullptr ? ldc_i(a.rope_row) : T;
-  const bool lng = T + 1 > kAttnShortMax;
   for (int u = blk; u < units; u += nblk) {
     const int s = u >> 1, j = u & 1;
     const bool own = s == ns - 1;   // slot T lies in the last split
-    bool done;
-    if (lng)
-      done = own ? attn_unit_long<true>(a, s, j, T, rrow, io) : attn_unit_long<false>(a, s, j, T, rrow, io);
-    else
+    bool done = false;
+    if (LONG && T + 1 > kAttnShortMax) {
+      if constexpr (LONG)
+        done = own ? attn_unit_long<true>(a, s, j, T, rrow, io) : attn_unit_long<false>(a, s, j, T, rrow, io);
+    } else {
       done = own ? attn_unit<true>(a, s, j, T, rrow, io) : attn_unit<false>(a, s, j, T, rrow, io);
+    }
     if (!done) return false;
   }
   return true;
@@ -2423,13 +2428,15 @@ __device__ __forceinline__ bool combine_long(const AttnArgs& a, int T, int blk, 
   return true;
 }
 
-template <class IO>
+template <class IO, bool LONG = true>
 __device__ __forceinline__ bool combine_body(const AttnArgs& a, int T, int blk, IO& io) {
   io.arrive();
   io.mark(0);   // trace: stage entry
   if (!io.wait()) return false;
+  if (!LONG && T + 1 > kAttnShortMax) return false;
   if (blk >= kCombineWGs || T < 0 || T >= a.max_ctx) return true;
-  if (T + 1 > kAttnShortMax) return combine_long(a, T, blk, io);
+  if constexpr (LONG)
+    if (T + 1 > kAttnShortMax) return combine_long(a, T, blk, io);
   const int h = blk >> 2, q = blk & 3;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int d = 64 * q + lane;
