@@ -284,19 +284,21 @@ def _gap(torch):
 
 
 def config_profile():
-    """{phase label: kernel us per call} and the workload line of the committed summary of a
-    kernel trace of this config section (CONFIG_PROFILE), or ({}, None)."""
-    out, wl = {}, None
+    """{phase label: kernel us per call}, and the workload and source lines, of the committed
+    summary of a kernel trace of this config section (CONFIG_PROFILE), or ({}, None, None)."""
+    out, wl, src = {}, None, None
     try:
         for line in open(CONFIG_PROFILE):
             if line.startswith("workload:"):
                 wl = line.split(":", 1)[1].strip()
+            elif line.startswith("source:"):
+                src = line.split(":", 1)[1].strip()
             elif line.startswith("config ") and "kernel_us_per_call" in line:
                 label = line[len("config "):line.index(":")]
                 out[label] = float(line.split("kernel_us_per_call")[1].split()[0])
     except OSError:
         pass
-    return out, wl
+    return out, wl, src
 
 
 def op_configs(q, torch, np, blob, idx, act_mode, with_c4=True):
@@ -311,19 +313,20 @@ def op_configs(q, torch, np, blob, idx, act_mode, with_c4=True):
     dev = torch.device("cuda")
     w8a8 = act_mode == "w8a8"
     rng = np.random.default_rng(7)
-    prof, prof_wl = config_profile()
+    prof, prof_wl, prof_src = config_profile()
     workload = f"act_mode={act_mode} rotate_bytes={ROTATE_BYTES} phases={','.join(CONFIG_PHASES)}"
+    matches = prof_wl == workload and prof_src == source_hash()
     out = {"workload": workload}
 
     def entry(label, nbytes, us, **kw):
         d = dict(_rate(nbytes, us), **kw)
-        k = prof.get(label) if prof_wl == workload else None
+        k = prof.get(label) if matches else None
         d["kernel_us"] = k
         if k:
             d["kernel_gbs"] = round(nbytes / (k * 1e-6) / 1e9, 1)
             d["kernel_frac"] = round(nbytes / (k * 1e-6) / 1e9 / PEAK_GBS, 4)
         d["kernel_source"] = ("profiles/op_configs_c1_c3_kernel_trace.md" if k else
-                              "none: the committed kernel trace is of another workload" if prof else
+                              "none: the committed kernel trace is of another workload or build" if prof else
                               "none: no committed kernel trace")
         return d
 
