@@ -68,7 +68,8 @@ class Golden:
 
     @staticmethod
     def silu(x):
-        return x / (1.0 + np.exp(-x, dtype=F32))
+        with np.errstate(over="ignore"):   # exp(-x) = inf below x = -88 gives the limit -0
+            return x / (1.0 + np.exp(-x, dtype=F32))
 
     @staticmethod
     def sigmoid(x):

@@ -25,8 +25,8 @@ import warnings
 
 import numpy as np
 
-KIND_NAMES = {0: "GEMV in_proj 1x8", 8: "GEMV q,k,v 1x8", 9: "GEMV gate,up 1x8", 1: "GEMV gated 2x1",
-              2: "GEMV 2x1", 3: "GEMV 4x1", 4: "DeltaNet",
+KIND_NAMES = {0: "GEMV in_proj 1x8", 8: "GEMV q,k,v 1x8", 9: "GEMV gate,up 1x8", 1: "GEMV out_proj (gated)",
+              2: "GEMV o_proj", 3: "GEMV down", 4: "DeltaNet",
               5: "attention", 6: "combine", 7: "LM head + argmax"}
 KIND_MARKS = {0: (1, 2, 5, 6), 8: (1, 2, 5, 6), 9: (1, 2, 5, 6), 1: (1, 2, 5, 6), 2: (1, 2, 5, 6), 3: (1, 2, 5, 6),
               4: (1, 2), 5: (1, 2), 6: (1,), 7: ()}
