@@ -123,6 +123,16 @@ __device__ __forceinline__ void permlane16_swap(unsigned& a, unsigned& b) {
   asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
 }
 
+// threadIdx.x, opaque to the optimiser.  A lane mask formed from it (a 64-bit
+// scalar register pair) is then formed where it is used: from threadIdx.x
+// itself the compiler hoists such masks out of the persistent kernel's stage
+// loop and holds them across every stage, which spills scalar registers.
+__device__ __forceinline__ int tid_here() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 // Lane l receives the value of lane l ^ OFF, with VALU instructions only (no
 // LDS round trip): quad permutations (DPP) for 1 and 2; row_half_mirror
 // (l ^ 7) then quad_perm [3,2,1,0] (l ^ 3) for 4; rotation of a 16-lane row by
@@ -142,10 +152,10 @@ __device__ __forceinline__ int xor_perm_i(int v) {
   unsigned a = (unsigned)v, b = (unsigned)v;
   if constexpr (OFF == 16) {
     permlane16_swap(a, b);   // a = v of the even row of each pair, b = v of the odd row
-    return (int)((threadIdx.x & 16) ? a : b);
+    return (int)((tid_here() & 16) ? a : b);
   }
   permlane32_swap(a, b);     // a = lower half of v (both halves), b = upper half
-  return (int)((threadIdx.x & 32) ? a : b);
+  return (int)((tid_here() & 32) ? a : b);
 }
 template <int OFF>
 __device__ __forceinline__ float xor_perm(float v) {

@@ -270,7 +270,7 @@ struct TagIO {
   __device__ __forceinline__ float* slot() { return lds_ring<kTagSlot>() + kTagSlot * (ring++ & 3); }
   uint64_t* tr = nullptr;     // optional timing trace of the current stage (points 0..2)
   __device__ __forceinline__ void mark(int p) {
-    if (tr != nullptr && threadIdx.x == 0) tr[p] = __builtin_amdgcn_s_memrealtime();
+    if (tr != nullptr && tid_here() == 0) tr[p] = __builtin_amdgcn_s_memrealtime();
   }
   __device__ __forceinline__ uint32_t tag(int st) const { return tag0 + (uint32_t)st; }
   __device__ __forceinline__ void arrive() {}
@@ -595,7 +595,10 @@ struct TagIO {
   // wave polls 64 samples spread over the vector before loading its pairs
   // again.  Ends with a barrier.
   __device__ __forceinline__ static bool vec_tags(const VecPoll& vp, int K, uint32_t tg) {
-    const int t = threadIdx.x;
+    // t < kPersistThreads (the persistent kernel's workgroup size): with the
+    // range stated, the bounds tests fold for K a multiple of 512 instead of
+    // becoming lane masks that the compiler holds across the stage loop
+    const int t = threadIdx.x & (kPersistThreads - 1);
     bool ok = true;
 #pragma unroll
     for (int i = 0; i < kL; ++i) {
@@ -624,9 +627,10 @@ struct TagIO {
       } while (!vec_tags(vp, K, tg));
       mark(4);   // trace: vector complete after a repoll
     }
+    const int tt = t & (kPersistThreads - 1);   // the same range statement as in vec_tags
 #pragma unroll
     for (int i = 0; i < kL; ++i) {
-      const int p = 2 * t + 2 * kPersistThreads * i;
+      const int p = 2 * tt + 2 * kPersistThreads * i;
       if (p < K) *reinterpret_cast<float2*>(lds + p) = make_float2(__uint_as_float(vp.u[i][0]), __uint_as_float(vp.u[i][2]));
     }
     __syncthreads();
