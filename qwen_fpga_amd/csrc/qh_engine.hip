@@ -153,6 +153,22 @@ struct Vec {
   int st = 0;
 };
 
+// DeltaNet layer li's in_proj rows: q, k, v (which the DeltaNet units wait
+// for), then z (only out_proj reads it), and the gate rows -- the longest work
+// of a workgroup -- on wave 0 of the last 2 kLH workgroups.  When the persistent
+// kernel keeps this layer's DeltaNet units (unit u on workgroup
+// (kLH kDnVQuarters li + u) mod grid) on the z workgroups, z goes first instead,
+// with the gate rows on its last workgroups, so that the units' workgroups
+// compute only q, k, v rows before the DeltaNet stage.  (One batch per wave:
+// batch b on workgroup b / 4.)
+bool dn_z_first(const qh_engine* e, int li) {
+  const int grid = e->persist_grid, units = kLH * kDnVQuarters;
+  const int qb = kConvDim / kRowsPerBatch, zb = kZDim / kRowsPerBatch;
+  if (grid * 4 != qb + zb || zb / 4 < 2 * kLH) return false;
+  const int first = (units * li) % grid;
+  return first + units > qb / 4;
+}
+
 // The stages of layers [l0, l1) of one decode step on the residual stream h
 // (updated to the last stage's output).  The tagged program leaves the device
 // StepCtl pointers out: the persistent kernel passes the token and position
@@ -187,17 +203,22 @@ void build_layers(const qh_engine* e, int l0, int l1, bool embed, Bufs& B, std::
         h = Vec{a.h_out, sA};
       }
       a.nseg = 2;   // the fp32 gate projections b, a run in the DeltaNet stage
-      a.seg[0] = mkseg(SEG_I8, E_CONV, kConvDim, 0, convd);
-      a.seg[0].w = i8p(e, l, R_QKV);
-      a.seg[0].sw = scp(e, l, R_QKV);
-      a.seg[0].c0 = f32p(e, l, R_CONV);
-      a.seg[0].c2 = e->conv + (size_t)li * kConvDim * kConvK;
-      a.seg[1] = mkseg(SEG_I8, E_SILU, kZDim, a.seg[0].nbatch, zb);   // silu(z) for the gated norm
-      a.seg[1].w = i8p(e, l, R_Z);
-      a.seg[1].sw = scp(e, l, R_Z);
+      const bool zfirst = tag && dn_z_first(e, li);
+      Seg& sq = a.seg[zfirst ? 1 : 0];
+      Seg& sz = a.seg[zfirst ? 0 : 1];
+      const int nzb = (kZDim + kRowsPerBatch - 1) / kRowsPerBatch, nqb = (kConvDim + kRowsPerBatch - 1) / kRowsPerBatch;
+      sq = mkseg(SEG_I8, E_CONV, kConvDim, zfirst ? nzb : 0, convd);
+      sq.w = i8p(e, l, R_QKV);
+      sq.sw = scp(e, l, R_QKV);
+      sq.c0 = f32p(e, l, R_CONV);
+      sq.c2 = e->conv + (size_t)li * kConvDim * kConvK;
+      sz = mkseg(SEG_I8, E_SILU, kZDim, zfirst ? 0 : nqb, zb);   // silu(z) for the gated norm
+      sz.w = i8p(e, l, R_Z);
+      sz.sw = scp(e, l, R_Z);
       if (tag) {   // the gates b, a of the 16 heads, from this prologue's activation
         a.gw = lanep(e, l, R_B);   // wb rows, then the wa rows (consecutive in lanes)
         a.grows = 2 * kLH;
+        a.gblk = zfirst ? nzb / 4 - 1 : -1;
         a.g_alog = f32p(e, l, R_ALOG);
         a.g_dtb = f32p(e, l, R_DTB);
         a.gout = B.at(convd, kConvDim);

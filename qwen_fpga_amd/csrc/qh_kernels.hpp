@@ -89,10 +89,11 @@ struct GemvArgs {
   int out_st = 0;               // this stage: tag of every output (segments and h_out)
   // DeltaNet gate rows (P_NORM, K = 1024; tagged in_proj): fp32 rows in the lane-interleaved
   // order, wb (beta, rows 0..15) then wa (g, rows 16..31); row r on wave 0 of workgroup
-  // nblk - 1 - r, from the prologue's activation.  Head h's g goes to pair 16 h of gout,
-  // beta to pair 16 h + 1 (deltanet.hpp:164-165).
+  // gblk - r (gblk < 0: nblk - 1), from the prologue's activation.  Head h's g goes to pair
+  // 16 h of gout, beta to pair 16 h + 1 (deltanet.hpp:164-165).
   const float* gw = nullptr;
   int grows = 0;
+  int gblk = -1;
   const float* g_alog = nullptr;
   const float* g_dtb = nullptr;
   float* gout = nullptr;

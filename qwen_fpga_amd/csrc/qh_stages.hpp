@@ -995,6 +995,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
   const int x_st = a.x_st, z_st = a.z_st, out_st = a.out_st;
   const float* const agw = a.gw;
   const int grows = a.grows;
+  const int gblk0 = a.gblk;
   const float* const ag_alog = a.g_alog;
   const float* const ag_dtb = a.g_dtb;
   float* const agout = a.gout;
@@ -1054,9 +1055,9 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, int blk, int nblk, 
         load16g(anw + (PRO == P_GATED ? ((16 * c) & 127) : 16 * c), nwv16[j]);
     }
   }
-  // a DeltaNet gate row (GemvArgs::gw), wave 0 of workgroups nblk - 1 - r
-  const int grow = nblk - 1 - blk;
-  const bool gate_wave = PRO == P_NORM && NCH == 1 && wave == 0 && grow < grows;
+  // a DeltaNet gate row (GemvArgs::gw), wave 0 of workgroups gblk - r
+  const int grow = (gblk0 >= 0 ? gblk0 : nblk - 1) - blk;
+  const bool gate_wave = PRO == P_NORM && NCH == 1 && wave == 0 && grow >= 0 && grow < grows;
   float gwv[16];
   float g_alog = 0.0f, g_dtb = 0.0f;   // the head's A_log and dt_bias (g rows only)
   if constexpr (PRO == P_NORM && NCH == 1) {
@@ -2345,10 +2346,14 @@ __device__ __forceinline__ bool attn_body(const AttnArgs& a, int T, int blk, int
   const int units = 2 * ns;
   io.arrive();
   if (!LONG && T + 1 > kAttnShortMax) return false;
-  if (blk >= units) return true;
+  // units from the last workgroup down: in the persistent kernel the q, k, v
+  // rows of the stage before run on the first workgroups, so the units'
+  // workgroups enter this stage (and issue their cache loads) early
+  const int r = nblk - 1 - blk;
+  if (r >= units) return true;
   io.mark(0);   // trace: stage entry
   const int rrow = a.rope_row != nullptr ? ldc_i(a.rope_row) : T;
-  for (int u = blk; u < units; u += nblk) {
+  for (int u = r; u < units; u += nblk) {
     const int s = u >> 1, j = u & 1;
     const bool own = s == ns - 1;   // slot T lies in the last split
     bool done = false;
