@@ -656,14 +656,17 @@ static void attn_core_ref(float* og, const float* q, const float* gate, const fl
   free(sc);
 }
 
-/* device order: positions in splits of DEV_ATTN_SPLIT; per split the score is a
- * C16 dot, m the split max, p = exp(s - m), l the 64-lane tree sum of p, acc the
- * k-ordered fma sum of p*v; the splits are merged sequentially with
+/* device order (qh_stages.hpp attn_unit / combine_body): the cached positions
+ * 0 .. Tn - 2 in splits of DEV_ATTN_SPLIT; per split the score is a C16 dot, m the
+ * split max, p = exp(s - m), l the 64-lane tree sum of p, acc the k-ordered fma sum
+ * of p*v.  The new position Tn - 1 is a split of its own after them, with m its
+ * score, l = 1 and acc its V row.  The splits are merged sequentially with
  * e_s = exp(m_s - M): L += l_s*e_s, acc += acc_s*e_s; ctx = acc * (1/L). */
 static void attn_core_dev(float* og, const float* q, const float* gate, const float* kcache,
                           const float* vcache, int Tn) {
   const int rep = NH / NKV, P = DEV_ATTN_SPLIT;
-  const int ns = (Tn + P - 1) / P;
+  const int Tc = Tn - 1;                  /* cached positions */
+  const int ns = (Tc + P - 1) / P + 1;    /* + the new position's split */
   float* ms = (float*)malloc(sizeof(float) * (size_t)ns);
   float* ls = (float*)malloc(sizeof(float) * (size_t)ns);
   float* accs = (float*)malloc(sizeof(float) * (size_t)ns * HD);
@@ -671,7 +674,14 @@ static void attn_core_dev(float* og, const float* q, const float* gate, const fl
     const int kv = h / rep;
     for (int s = 0; s < ns; ++s) {
       float sc[DEV_ATTN_SPLIT], p[64];
-      const int t0 = s * P, t1 = t0 + P < Tn ? t0 + P : Tn;
+      if (s == ns - 1) {   /* the new position: m = its score, l = 1, acc = its V row */
+        const float* vrow = vcache + (long)Tc * KV_PROJ + kv * HD;
+        ms[s] = c16_dot_f32(q + h * HD, kcache + (long)Tc * KV_PROJ + kv * HD, HD) * 0.0625f;
+        ls[s] = 1.0f;
+        for (int d = 0; d < HD; ++d) accs[(size_t)s * HD + d] = vrow[d];
+        continue;
+      }
+      const int t0 = s * P, t1 = t0 + P < Tc ? t0 + P : Tc;
       float m = -INFINITY;
       for (int t = t0; t < t1; ++t) {
         const float d = c16_dot_f32(q + h * HD, kcache + (long)t * KV_PROJ + kv * HD, HD) * 0.0625f;
