@@ -1943,6 +1943,14 @@ __device__ __forceinline__ void load16_rs(const __amdgpu_buffer_rsrc_t& rs, int 
   }
 }
 
+// Cache rows are read with ordinary loads.  A row is written once per launch,
+// with sc1 (write-through) stores, by the combine (or, above kAttnShortMax
+// positions, by the owner of the split holding it), possibly on another XCD,
+// and complete before the token's head partial is published.  Before that
+// token no unit reads the row (rows are clamped to T - 1), so no other XCD's
+// L2 holds a stale copy; the owner of a long split loads the row of slot T,
+// replaces it in registers and writes it through its own L2.  Across launches
+// the kernel boundary orders it.
 // Straight-line loads, no branch: rows at or past slot T are clamped to row
 // T - 1 (T = 0: an empty descriptor, reads 0).  Such a K row only meets a
 // score that is masked to -inf, and such a V row lies past the positions the
