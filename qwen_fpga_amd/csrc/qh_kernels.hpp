@@ -22,12 +22,21 @@ __host__ __device__ constexpr int attn_split_len(int Tn) {
                                     ? 4 * ((Tn + 4 * kAttnMaxSplits - 1) / (4 * kAttnMaxSplits))
                                     : kAttnMaxSplitLen);
 }
-__host__ __device__ constexpr int attn_nsplit(int Tn) { return (Tn + attn_split_len(Tn) - 1) / attn_split_len(Tn); }
+// Splits of a context of Tn positions: up to kAttnShortMax the Tn - 1 cached
+// positions in splits of kAttnSplit, then the new position as a split of its
+// own (at most 129); above, splits of attn_split_len(Tn) (at most kAttnMaxSplits).
+__host__ __device__ constexpr int attn_nsplit(int Tn) {
+  return Tn <= kAttnShortMax ? (Tn - 1 + kAttnSplit - 1) / kAttnSplit + 1
+                             : (Tn + attn_split_len(Tn) - 1) / attn_split_len(Tn);
+}
 // the most splits any context up to max_ctx positions takes (buffer sizes)
 __host__ __device__ constexpr int attn_nsplit_max(int max_ctx) {
-  return max_ctx <= kAttnShortMax ? (max_ctx + kAttnSplit - 1) / kAttnSplit
-                                  : (attn_nsplit(max_ctx) > kAttnMaxSplits ? attn_nsplit(max_ctx) : kAttnMaxSplits);
+  return max_ctx <= kAttnShortMax ? attn_nsplit(max_ctx)
+                                  : (attn_nsplit(kAttnShortMax) > kAttnMaxSplits ? attn_nsplit(kAttnShortMax)
+                                                                                 : kAttnMaxSplits);
 }
+static_assert(attn_nsplit(kAttnShortMax) == kAttnMaxSplits + 1 && attn_nsplit(kAttnShortMax + 1) <= kAttnMaxSplits,
+              "split counts at the short / long boundary");
 constexpr int kDnVQuarters = 4;      // DeltaNet workgroups per head (32 v columns each)
 constexpr int kDnSlots = 5;          // persistent kernel: DeltaNet state tiles per workgroup (LDS)
 

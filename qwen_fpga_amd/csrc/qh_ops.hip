@@ -90,7 +90,7 @@ constexpr size_t attention_scratch_bytes(int ns) {
 // device current) and only that address reaches kernels.
 constexpr int kNoallocMaxCtx = 65536;
 constexpr size_t kNoallocBytes = attention_scratch_bytes(attn_nsplit_max(kNoallocMaxCtx));
-static_assert(attn_nsplit_max(kNoallocMaxCtx) == kAttnMaxSplits && kNoallocBytes < (size_t)2 << 20,
+static_assert(attn_nsplit_max(kNoallocMaxCtx) == kAttnMaxSplits + 1 && kNoallocBytes < (size_t)2 << 20,
               "a modest, fixed maximum");
 __device__ __align__(256) char scratch[kNoallocBytes];
 constexpr int kMaxDevices = 64;

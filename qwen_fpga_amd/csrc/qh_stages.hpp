@@ -1944,8 +1944,9 @@ __device__ __forceinline__ void load16_rs(const __amdgpu_buffer_rsrc_t& rs, int 
 }
 
 // Cache rows are read with ordinary loads.  A row is written once per launch,
-// with sc1 (write-through) stores, by the combine (or, above kAttnShortMax
-// positions, by the owner of the split holding it), possibly on another XCD,
+// with sc1 (write-through) stores, by the new position's unit (or, above
+// kAttnShortMax positions, by the owner of the split holding it), possibly on
+// another XCD,
 // and complete before the token's head partial is published.  Before that
 // token no unit reads the row (rows are clamped to T - 1), so no other XCD's
 // L2 holds a stale copy; the owner of a long split loads the row of slot T,
@@ -2004,7 +2005,7 @@ __device__ __forceinline__ void qk_norm_rope(float* x, const float* nw16, float 
 
 // Contexts up to kAttnShortMax: unit (split s, kv head j) over the cached
 // positions t0 .. min(t0 + 16, T) - 1; position T itself (the new K and V rows,
-// attention.hpp:45-54) is the combine's, as a split of its own.  The poll of the
+// attention.hpp:45-54) is a split of its own (attn_new_pos).  The poll of the
 // query is issued first and the prefetch after it, so the poll does not queue
 // behind the cache rows.
 template <class IO>
@@ -2070,6 +2071,58 @@ __device__ __forceinline__ bool attn_unit(const AttnArgs& a, int s, int j, int T
     }
   }
   io.st4(a.pacc, a.part_st, (h * a.nsplit_max + s) * 256 + 4 * lane, acc);
+  return true;
+}
+
+// The new position T of kv head j, contexts up to kAttnShortMax: the last
+// split (index sidx of the partials) with m = its score, l = 1 and acc = its V
+// row.  Wave i takes query head 4 j + i: it fetches the query and the new K and
+// V rows (six regions), normalises and rotates q and K (attention.hpp:39-50)
+// and forms the score; wave 0 writes the new cache rows (attention.hpp:46-54).
+template <class IO>
+__device__ __forceinline__ bool attn_new_pos(const AttnArgs& a, int sidx, int j, int T, int rrow, IO& io) {
+  constexpr int kBig = 0x7ffffff0;
+  const int lane = threadIdx.x & 63, g16 = lane & 15, pg = lane >> 4;
+  const int i = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = 4 * j + i;
+  const int reg[6] = {h * 512, h * 512 + 128, 4096 + j * 256, 4096 + j * 256 + 128, 4608 + j * 256, 4608 + j * 256 + 128};
+  const int iv[1] = {h * 512 + lane};
+  typename IO::template PollR<6, 1> P;
+  io.template pollr_issue<6, 1>(a.qkv, reg, iv, P);
+  float qn16[16], kn16[16], cs16[16], sn16[16];
+  load16_rs(rsrc_n(a.qn, kBig), 64 * g16, qn16);
+  load16_rs(rsrc_n(a.kn, kBig), 64 * g16, kn16);
+  {
+    const __amdgpu_buffer_rsrc_t rr = rsrc_n(a.rope, kBig);
+    load16_rs(rr, (rrow * 64 + 16 * (g16 & 1)) * 4, cs16);
+    load16_rs(rr, (rrow * 64 + 32 + 16 * (g16 & 1)) * 4, sn16);
+  }
+  if (!io.wait()) return false;
+  float* wa = wave_area();
+  float unused[1];
+  if (!io.template pollr_finish<6, 1>(a.qkv, a.qkv_st, reg, iv, P, wa, unused)) return false;
+  float qv[16], kv[16], v4[4];
+  load16l(wa + 16 * g16, qv);         // query dims 16 g16 .. + 15
+  load16l(wa + 256 + 16 * g16, kv);   // new K row, same dims
+  {
+    const f32x4 t = *as_lds(reinterpret_cast<const f32x4*>(wa + 512 + 4 * lane));   // new V row, dims 4 lane ..
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v4[e] = t[e];
+  }
+  io.mark(1);   // trace: q and the new k, v received
+  qk_norm_rope(qv, qn16, a.eps, g16, cs16, sn16);
+  qk_norm_rope(kv, kn16, a.eps, g16, cs16, sn16);
+  if (i == 0) {
+    if (pg == 0) stc16(a.kc, T * 512 + j * 256 + 16 * g16, kv);
+    stc4(a.vc, T * 512 + j * 256 + 4 * lane, v4);
+  }
+  const float sc = xor_sum<16>(dot16_f32(qv, kv, 0.0f)) * 0.0625f;
+  if (lane == 0) {
+    io.st1(a.pm, a.part_st, h * a.nsplit_max + sidx, sc);
+    io.st1(a.pl, a.part_st, h * a.nsplit_max + sidx, 1.0f);
+  }
+  io.mark(2);   // trace: score formed
+  io.st4(a.pacc, a.part_st, (h * a.nsplit_max + sidx) * 256 + 4 * lane, v4);
   return true;
 }
 
@@ -2322,8 +2375,7 @@ template <class IO, bool LONG = true>
 __device__ __forceinline__ bool attn_body(const AttnArgs& a, int T, int blk, int nblk, IO& io) {
   const bool ok = T >= 0 && T < a.max_ctx;
   const bool lng = T + 1 > kAttnShortMax;
-  // short contexts: splits of the T cached positions (position T is the combine's)
-  const int ns = !ok ? 0 : lng ? attn_nsplit(T + 1) : (T + kAttnSplit - 1) / kAttnSplit;
+  const int ns = ok ? attn_nsplit(T + 1) : 0;   // short contexts: the last split is position T alone
   const int units = 2 * ns;
   io.arrive();
   if (!LONG && T + 1 > kAttnShortMax) return false;
@@ -2335,15 +2387,17 @@ __device__ __forceinline__ bool attn_body(const AttnArgs& a, int T, int blk, int
   io.mark(0);   // trace: stage entry
   const int rrow = a.rope_row != nullptr ? ldc_i(a.rope_row) : T;
   for (int u = r; u < units; u += nblk) {
-    const int s = u >> 1, j = u & 1;
     bool done = false;
     if (LONG && lng) {
       if constexpr (LONG) {
+        const int s = u >> 1, j = u & 1;
         const bool own = s == ns - 1;   // slot T lies in the last split
         done = own ? attn_unit_long<true>(a, s, j, T, rrow, io) : attn_unit_long<false>(a, s, j, T, rrow, io);
       }
+    } else if (u < 2) {   // the new position's split (units 0, 1: the most idle workgroups)
+      done = attn_new_pos(a, ns - 1, u, T, rrow, io);
     } else {
-      done = attn_unit(a, s, j, T, rrow, io);
+      done = attn_unit(a, (u - 2) >> 1, u & 1, T, rrow, io);
     }
     if (!done) return false;
   }
@@ -2428,64 +2482,20 @@ __device__ __forceinline__ bool combine_body(const AttnArgs& a, int T, int blk, 
   if (blk >= kCombineWGs || T < 0 || T >= a.max_ctx) return true;
   if constexpr (LONG)
     if (T + 1 > kAttnShortMax) return combine_long(a, T, blk, io);
-  const int h = blk >> 2, q = blk & 3, j = h >> 2;   // query head, 64-dimension quarter, kv head
+  const int h = blk >> 2, q = blk & 3;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g16 = lane & 15, pg = lane >> 4;
   const int d = 64 * q + lane;
-  const int ns = (T + kAttnSplit - 1) / kAttnSplit;   // splits of the T cached positions
+  const int ns = attn_nsplit(T + 1);   // the last split is position T alone
   const int base = h * a.nsplit_max;
   const Raw graw = io.issue1(a.qkv, h * 512 + 256 + d, wave == 0);   // the output gate of dimension d
   float* buf = io.slot();   // [kCombineChunk splits][64 dimensions]
   float M = -__builtin_inff();
-  // Position T, a split of its own (m = its score, l = 1, acc = its V row), folded
-  // after the others: wave 0 takes the query of head h, the new K row of kv head
-  // j and the 128-dimension half of its V row that holds this quarter, normalises
-  // and rotates q and K (attention.hpp:39-50) and forms the score.  The four
-  // workgroups of the kv head's first query head write the new cache rows, a
-  // quarter each.  The inputs are the q, k, v stage's, so this runs while the
-  // attention units do.
-  float sT = 0.0f, vT = 0.0f;
   if (wave == 0) {
-    constexpr int kBig = 0x7ffffff0;
-    const int reg[5] = {h * 512, h * 512 + 128, 4096 + j * 256, 4096 + j * 256 + 128, 4608 + j * 256 + 128 * (q >> 1)};
-    const int iv[1] = {h * 512 + lane};
-    typename IO::template PollR<5, 1> P;
-    io.template pollr_issue<5, 1>(a.qkv, reg, iv, P);
-    const int rrow = a.rope_row != nullptr ? ldc_i(a.rope_row) : T;
-    float qn16[16], kn16[16], cs16[16], sn16[16];
-    load16_rs(rsrc_n(a.qn, kBig), 64 * g16, qn16);
-    load16_rs(rsrc_n(a.kn, kBig), 64 * g16, kn16);
-    {
-      const __amdgpu_buffer_rsrc_t rr = rsrc_n(a.rope, kBig);
-      load16_rs(rr, (rrow * 64 + 16 * (g16 & 1)) * 4, cs16);
-      load16_rs(rr, (rrow * 64 + 32 + 16 * (g16 & 1)) * 4, sn16);
-    }
-    float* wa = wave_area();
-    float unused[1];
-    if (!io.template pollr_finish<5, 1>(a.qkv, a.qkv_st, reg, iv, P, wa, unused)) return false;
-    float qv[16], kv[16];
-    load16l(wa + 16 * g16, qv);         // query dims 16 g16 .. + 15
-    load16l(wa + 256 + 16 * g16, kv);   // new K row, same dims
-    const float* vh = wa + 512 - 128 * (q >> 1);   // new V row from dimension 128 (q >> 1)
-    vT = vh[d];
-    qk_norm_rope(qv, qn16, a.eps, g16, cs16, sn16);
-    qk_norm_rope(kv, kn16, a.eps, g16, cs16, sn16);
-    sT = xor_sum<16>(dot16_f32(qv, kv, 0.0f)) * 0.0625f;
-    if ((h & 3) == 0) {   // the new cache rows of slot T (attention.hpp:46-54), dimensions 64 q .. + 63
-      if (pg == 0 && (g16 >> 2) == q) stc16(a.kc, T * 512 + j * 256 + 16 * g16, kv);
-      if (lane < 16) {
-        float v4[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v4[e] = vh[64 * q + 4 * lane + e];
-        stc4(a.vc, T * 512 + j * 256 + 64 * q + 4 * lane, v4);
-      }
-    }
     for (int s0 = 0; s0 < ns; s0 += 64) {
       float mv;
       if (!io.ld1(a.pm, a.part_st, base + min(s0 + lane, ns - 1), mv)) return false;
       M = fmaxf(M, xor_max<64>(mv));
     }
-    M = fmaxf(M, sT);
   }
   float L = 0.0f, ctx = 0.0f;
   constexpr int kPer = kCombineChunk / 4;
@@ -2517,11 +2527,6 @@ __device__ __forceinline__ bool combine_body(const AttnArgs& a, int T, int blk, 
     __syncthreads();
   }
   if (wave != 0) return true;
-  {   // position T
-    const float eT = dev_expf(sT - M);
-    L = L + 1.0f * eT;
-    ctx = ctx + vT * eT;
-  }
   io.mark(1);   // trace: all split partials folded
   const float invL = 1.0f / L;
   float gate;
