@@ -67,7 +67,7 @@ hipError_t launch_gemv(const GemvArgs& a, int waves_per_block, hipStream_t s) {
 
 __global__ __launch_bounds__(256) void head_kernel(const HeadArgs a) {
   PlainIO io{a.done};
-  head_body(a, blockIdx.x, gridDim.x, io, a.logits);
+  head_body<true>(a, blockIdx.x, gridDim.x, io, a.logits);
 }
 
 hipError_t launch_head(const HeadArgs& a, int grid, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {

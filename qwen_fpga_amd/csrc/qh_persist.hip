@@ -111,7 +111,7 @@ __global__ __launch_bounds__(kPersistThreads) void persist_kernel(const PersistA
         case ST_DELTANET: ok = deltanet_all(st.d, blk, nblk, io, tok); break;
         case ST_ATTN: ok = attn_body<TagIO, LONG>(st.at, pos, blk, nblk, io); break;
         case ST_COMBINE: ok = combine_body<TagIO, LONG>(st.at, pos, blk, io); break;
-        default: ok = head_body(st.hd, blk, nblk, io, P.logits); break;
+        default: ok = head_body<false>(st.hd, blk, nblk, io, P.logits); break;
       }
       if (tr != nullptr && t == 0) tr[kTraceSlots - 1] = __builtin_amdgcn_s_memrealtime();
       if (!ok) io.failed = true;   // the stage body refused its arguments: same exit

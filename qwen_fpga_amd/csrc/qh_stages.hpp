@@ -932,6 +932,19 @@ __device__ __forceinline__ Seg seg_uniform(const Seg& s) {
 // int8 rows: its descriptors are empty and the loads read nothing.  g and row0
 // are wave-uniform: a row's byte offset goes in the scalar offset of the
 // buffer load, and only the lane's chunk offset is per lane.
+// Cache policy of a GEMV stage's weight loads (EM: the stage kind's epilogue
+// set).  The gate/up weights (176 MB over the 24 layers) and the attention
+// q, k, v weights (31 MB) load with the default policy, so they stay in the
+// 256 MB Infinity Cache from one token to the next.  Every other weight byte
+// (in_proj, the 1024-row projections and, in the persistent kernel, the LM
+// head: 545 MB, each read once per token) loads non-temporally so that it does
+// not evict them.  More than that does not fit: adding in_proj (327 MB cached)
+// or half the head (334 MB) made the decode slower than caching less.
+template <int EM>
+constexpr int weight_policy() {
+  return (EM == kEmSwiglu || EM == kEmStore) ? 0 : kNt;
+}
+
 template <int NCH, int R, int EM>
 __device__ __forceinline__ void load_batch(const Seg& g, int row0, int K, int nchunk, int lane,
                                            uint32_t (&w)[NCH][R][4]) {
@@ -950,10 +963,7 @@ __device__ __forceinline__ void load_batch(const Seg& g, int row0, int K, int nc
     const int roff = __builtin_amdgcn_readfirstlane((pair ? (row >> 1) : row) * K);
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
-      // non-temporal: a weight byte is read once per token, and 503 MB of them
-      // would otherwise evict from the 256 MB Infinity Cache what is read again
-      // soon (the LM head, the recurrent state, the KV cache)
-      const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(second ? rw2 : rw, voff[j], roff, kNt);
+      const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(second ? rw2 : rw, voff[j], roff, weight_policy<EM>());
       w[j][r][0] = t[0];
       w[j][r][1] = t[1];
       w[j][r][2] = t[2];
@@ -1532,6 +1542,11 @@ __device__ __forceinline__ bool gemv_splitk(const GemvArgs& a, int blk, IO& io) 
 // order, running argmax with the reference's rule (strict >, so the first
 // index wins a tie; qwen_synth.hpp:81-88) folded per workgroup.  Two batches
 // of 8 rows (16 KiB per wave) are in flight while a third is reduced.
+// KEEP: every other batch loads with the default cache policy, so half the
+// head stays in the Infinity Cache from one token to the next (the layer
+// kernels' decode, whose weights all load non-temporally).  The persistent
+// kernel loads the whole head non-temporally: its Infinity Cache holds the
+// gate/up and q, k, v weights instead (weight_policy).
 // ===========================================================================
 __device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
   if (v > bv || (v == bv && i < bi)) {
@@ -1566,7 +1581,7 @@ __device__ __forceinline__ void head_load(const int8_t* hw, const float* hsw, in
   sc = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (bb * 8 + rl) * 4, 0, 0));
 }
 
-template <class IO>
+template <bool KEEP, class IO>
 __device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, IO& io, float* logits) {
   const int lane = threadIdx.x & 63, nwv = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1582,7 +1597,7 @@ __device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, 
   uint32_t w0[8][4], w1[8][4];
   float sc0 = 0.0f, sc1 = 0.0f;
   head_load<kNt>(hw, hsw, b, total, lane, rl, w0, sc0);   // two batches in flight before the norm prologue
-  head_load<0>(hw, hsw, b + stride, total, lane, rl, w1, sc1);
+  head_load<KEEP ? 0 : kNt>(hw, hsw, b + stride, total, lane, rl, w1, sc1);
   float xv[16], nw[16];
   if (a.nw_lanes)
     load16c(a.nw, lane, nw);
@@ -1620,7 +1635,7 @@ __device__ __forceinline__ bool head_body(const HeadArgs& a, int blk, int nblk, 
     }
   };
   using Nt = std::integral_constant<int, kNt>;
-  using Keep = std::integral_constant<int, 0>;
+  using Keep = std::integral_constant<int, KEEP ? 0 : kNt>;
   for (; b + stride < total; b += 2 * stride) {
     batch(Nt{}, b, w0, sc0);
     batch(Keep{}, b + stride, w1, sc1);
