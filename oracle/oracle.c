@@ -42,7 +42,7 @@
 #define DEV_ATTN_SHORT_MAX 2048
 #define DEV_ATTN_MAX_SPLITS 128
 #define DEV_ATTN_MAX_SPLIT_LEN 512
-#define DEV_ATTN_LONG_D 4
+#define DEV_ATTN_LONG_D 2
 #define DEV_DN_KGROUPS 8
 
 static int is_linear(int layer) { return (layer % 4) != 3; }   /* types.hpp:47 */

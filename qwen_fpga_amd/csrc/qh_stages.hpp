@@ -2161,7 +2161,11 @@ __device__ __forceinline__ bool attn_new_pos(const AttnArgs& a, int sidx, int j,
 // The loads stay straight-line: each unrolled step uses the rows loaded
 // kAttnLongD steps earlier and issues the loads of kAttnLongD steps later.
 // ===========================================================================
-constexpr int kAttnLongD = 4;   // iterations of K rows in flight per wave (V: 4 rows per iteration)
+// Iterations of K rows in flight per wave (V: 4 rows per iteration).  Two:
+// the C3 layer at T = 32768 took 47.6 us with 2, 48.4 with 3, 50.1 with 4 and
+// 56.2 with 8 (each wave's iterations are padded to a multiple of this, and
+// the padded steps still read rows), 50.8 with 1.
+constexpr int kAttnLongD = 2;
 
 template <bool OWNER, class IO>
 __device__ __forceinline__ bool attn_unit_long(const AttnArgs& a, int s, int j, int T, int rrow, IO& io) {
